@@ -1,0 +1,230 @@
+"""ctypes bindings for the CPU oracle (oracle/talos_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP backend and the CPU
+baseline timed beside it.  Only tests/, the smoke check and bench.py's
+cpu_baseline leg load it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libtalos_oracle.so")
+
+F32, Q4_0, Q8_0, Q6_K = 0, 2, 8, 14
+_F = C.POINTER(C.c_float)
+_U8 = C.POINTER(C.c_uint8)
+
+
+class Config(C.Structure):
+    _fields_ = [("n_layer", C.c_uint32), ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32),
+                ("n_embd", C.c_uint32), ("n_ff", C.c_uint32), ("context_length", C.c_uint32),
+                ("vocab_size", C.c_uint32), ("rope_dim", C.c_uint32), ("rms_eps", C.c_float),
+                ("rope_freq_base", C.c_float)]
+
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        sig = {
+            "tor_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "tor_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "tor_dequantize": (None, [C.c_int, _U8, _F, C.c_size_t]),
+            "tor_quantize_q8_0": (None, [_F, _U8, C.c_size_t]),
+            "tor_quantize_q4_0": (None, [_F, _U8, C.c_size_t]),
+            "tor_quantize_q6_k": (None, [_F, _U8, C.c_size_t]),
+            "tor_dot": (C.c_float, [_F, _F, C.c_size_t]),
+            "tor_matvec_f32": (None, [_F, _F, _F, C.c_size_t, C.c_size_t, C.c_int]),
+            "tor_matvec_quant": (None, [_U8, C.c_int, _F, _F, C.c_size_t, C.c_size_t, C.c_int]),
+            "tor_rmsnorm": (None, [_F, _F, C.c_float, _F, C.c_size_t]),
+            "tor_softmax": (None, [_F, C.c_size_t]),
+            "tor_silu": (C.c_float, [C.c_float]),
+            "tor_swiglu": (None, [_F, _F, _F, C.c_size_t]),
+            "tor_rope": (None, [_F, C.c_size_t, C.c_size_t, C.c_size_t, C.c_float]),
+            "tor_argmax": (C.c_uint32, [_F, C.c_size_t]),
+            "tor_model_load": (C.c_void_p, [C.c_void_p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
+            "tor_model_free": (None, [C.c_void_p]),
+            "tor_model_config": (None, [C.c_void_p, C.POINTER(Config)]),
+            "tor_model_cap_context": (None, [C.c_void_p, C.c_size_t]),
+            "tor_model_set_threads": (None, [C.c_void_p, C.c_int]),
+            "tor_model_forward": (C.c_int, [C.c_void_p, C.c_uint32, C.c_size_t, _F]),
+            "tor_model_forward_hidden": (C.c_int, [C.c_void_p, C.c_uint32, C.c_size_t, _F]),
+            "tor_model_reset": (None, [C.c_void_p]),
+            "tor_model_kv_len": (C.c_size_t, [C.c_void_p]),
+            "tor_model_set_kv": (C.c_int, [C.c_void_p, _F, _F, C.c_size_t]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    return a.ctypes.data_as(_F)
+
+
+def _u8(a):
+    return a.ctypes.data_as(_U8)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().tor_f16_to_f32(h)
+
+
+def f32_to_f16(f: float) -> int:
+    return lib().tor_f32_to_f16(f)
+
+
+def block(t):
+    return {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q6_K: (256, 210)}[t]
+
+
+def dequantize(t: int, raw: np.ndarray, n: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    lib().tor_dequantize(t, _u8(raw), _f(out), n)
+    return out
+
+
+def quantize(t: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    be, bb = block(t)
+    out = np.zeros(x.size // be * bb, np.uint8)
+    fn = {Q8_0: lib().tor_quantize_q8_0, Q4_0: lib().tor_quantize_q4_0, Q6_K: lib().tor_quantize_q6_k}[t]
+    fn(_f(x), _u8(out), x.size)
+    return out
+
+
+def matvec(t: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, nthreads: int = 1) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(rows, np.float32)
+    if t == F32:
+        ww = np.ascontiguousarray(w, dtype=np.float32)
+        lib().tor_matvec_f32(_f(ww), _f(x), _f(out), rows, cols, nthreads)
+    else:
+        ww = np.ascontiguousarray(w, dtype=np.uint8)
+        lib().tor_matvec_quant(_u8(ww), t, _f(x), _f(out), rows, cols, nthreads)
+    return out
+
+
+def dot(a, b) -> float:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().tor_dot(_f(a), _f(b), a.size)
+
+
+def rmsnorm(x, w, eps) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().tor_rmsnorm(_f(x), _f(w), eps, _f(out), x.size)
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    x = np.array(x, np.float32)
+    lib().tor_softmax(_f(x), x.size)
+    return x
+
+
+def silu(x: float) -> float:
+    return lib().tor_silu(x)
+
+
+def swiglu(g, u) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    out = np.empty_like(g)
+    lib().tor_swiglu(_f(g), _f(u), _f(out), g.size)
+    return out
+
+
+def rope(v, pos, n_head, head_dim, freq_base) -> np.ndarray:
+    v = np.array(v, np.float32)
+    lib().tor_rope(_f(v), pos, n_head, head_dim, freq_base)
+    return v
+
+
+def argmax(logits) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().tor_argmax(_f(logits), logits.size)
+
+
+class OracleModel:
+    """Model::forward on the CPU (src/model/llama.rs:85-183).  The GGUF bytes
+    must outlive this object; pass (address, length) of memory the caller
+    keeps alive, or a bytes object (kept referenced here)."""
+
+    def __init__(self, data, nthreads: int = 1):
+        if isinstance(data, (bytes, bytearray, np.ndarray)):
+            self._keep = np.ascontiguousarray(np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray)
+                                              else data, np.uint8)
+            addr, n = self._keep.ctypes.data, self._keep.size
+        else:
+            addr, n = data
+            self._keep = None
+        err = C.create_string_buffer(512)
+        h = lib().tor_model_load(C.c_void_p(addr), n, nthreads, err, 512)
+        if not h:
+            raise RuntimeError(err.value.decode())
+        self._h = h
+        cfg = Config()
+        lib().tor_model_config(self._h, C.byref(cfg))
+        self.cfg = cfg
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().tor_model_free(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def set_threads(self, n):
+        lib().tor_model_set_threads(self._h, n)
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.cfg.vocab_size, np.float32)
+        if lib().tor_model_forward(self._h, token, pos, _f(out)):
+            raise RuntimeError("oracle forward failed")
+        return out
+
+    def forward_hidden(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.cfg.n_embd, np.float32)
+        if lib().tor_model_forward_hidden(self._h, token, pos, _f(out)):
+            raise RuntimeError("oracle forward failed")
+        return out
+
+    def reset(self):
+        lib().tor_model_reset(self._h)
+
+    def cap_context(self, n):
+        lib().tor_model_cap_context(self._h, n)
+        cfg = Config()
+        lib().tor_model_config(self._h, C.byref(cfg))
+        self.cfg = cfg
+
+    def kv_len(self) -> int:
+        return lib().tor_model_kv_len(self._h)
+
+    def set_kv(self, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        lib().tor_model_set_kv(self._h, _f(k), _f(v), k.shape[1])

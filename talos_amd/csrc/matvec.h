@@ -1,0 +1,246 @@
+// matvec.h -- fused dequant-matvec cores for batch-1 decode (gfx950).
+//
+// Restates the arithmetic of the reference's CPU matvec (src/math/matmul.rs:
+// 15-47 for F32, src/math/quant.rs:18-51 for the block formats, whose
+// dequantize is src/gguf/dtype.rs:64-121) as a bandwidth-bound GEMV:
+//
+//  * one wavefront computes two output rows that share x; lane l consumes
+//    chunks l, l+64, ... of both rows (one 128-bit load per row per chunk);
+//  * x lives in LDS with a 16-B pad every 32 (or 64) floats so the strided
+//    per-lane 128-bit reads are bank-conflict free;
+//  * the quant offset (-8 for Q4_0, -128 for the xor-ed Q8_0 bytes, -32 for
+//    Q6_K) is folded out through the sum of x over each 16-element group:
+//    sum((q-o)x) = sum(qx) - o*sum(x), so each weight costs one byte->float
+//    convert and one FMA;
+//  * fp32 accumulation, one scale multiply per block, a fixed-order
+//    butterfly across lanes at the end.  No MFMA: batch-1 is HBM-bound.
+#pragma once
+#include "device_common.h"
+#include "layout.h"
+
+// LDS index of x element e in layout L (0: pad 4 floats per 32; 1: per 64).
+template <int L>
+__device__ __forceinline__ int xidx(int e) {
+  return L == 0 ? e + ((e >> 5) << 2) : e + ((e >> 6) << 2);
+}
+static inline __host__ __device__ int xlds_floats(int n, int L) {
+  n = (n + 15) & ~15;
+  return L == 0 ? n + (n >> 5) * 4 + 4 : n + (n >> 6) * 4 + 4;
+}
+
+__device__ __forceinline__ f4 lds4(const float* xs, int i) {
+  return *reinterpret_cast<const f4*>(xs + i);
+}
+
+__device__ __forceinline__ u4 ldg4(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+}
+
+// ---- per-format chunk dots.  Each adds the dot of one chunk of row A (and
+// row B when `two`) with x onto accA / accB.
+
+__device__ __forceinline__ void chunk_f32(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
+                                          bool two, const float* xs, int c, float& accA, float& accB) {
+  const f4 x = lds4(xs, xidx<0>(c * 4));
+  const size_t stride = (size_t)A.nchunk * 16;  // rows padded to a multiple of 16 floats
+  const u4 wa = ldg4(A.q + ra * stride + (size_t)c * 16);
+  f4 fa = __builtin_bit_cast(f4, wa);
+  accA = __builtin_fmaf(fa.x, x.x, accA);
+  accA = __builtin_fmaf(fa.y, x.y, accA);
+  accA = __builtin_fmaf(fa.z, x.z, accA);
+  accA = __builtin_fmaf(fa.w, x.w, accA);
+  if (two) {
+    const u4 wb = ldg4(B.q + rb * stride + (size_t)c * 16);
+    f4 fb = __builtin_bit_cast(f4, wb);
+    accB = __builtin_fmaf(fb.x, x.x, accB);
+    accB = __builtin_fmaf(fb.y, x.y, accB);
+    accB = __builtin_fmaf(fb.z, x.z, accB);
+    accB = __builtin_fmaf(fb.w, x.w, accB);
+  }
+}
+
+__device__ __forceinline__ float q4_block_dot(u4 q, const f4* x, float xs8) {
+  float s = 0.f;
+  s = dot_ub4(q.x & 0x0F0F0F0Fu, x[0], s);
+  s = dot_ub4(q.y & 0x0F0F0F0Fu, x[1], s);
+  s = dot_ub4(q.z & 0x0F0F0F0Fu, x[2], s);
+  s = dot_ub4(q.w & 0x0F0F0F0Fu, x[3], s);
+  float t = 0.f;
+  t = dot_ub4((q.x >> 4) & 0x0F0F0F0Fu, x[4], t);
+  t = dot_ub4((q.y >> 4) & 0x0F0F0F0Fu, x[5], t);
+  t = dot_ub4((q.z >> 4) & 0x0F0F0F0Fu, x[6], t);
+  t = dot_ub4((q.w >> 4) & 0x0F0F0F0Fu, x[7], t);
+  return (s + t) - xs8;
+}
+
+__device__ __forceinline__ void chunk_q4_0(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
+                                           bool two, const float* xs, const float* xsum, int c,
+                                           float& accA, float& accB) {
+  const size_t nc = A.nchunk;
+  const u4 qa = ldg4(A.q + (ra * nc + c) * 16);
+  const float da = f16_to_f32(A.d[ra * nc + c]);
+  u4 qb;
+  float db = 0.f;
+  if (two) {
+    qb = ldg4(B.q + (rb * nc + c) * 16);
+    db = f16_to_f32(B.d[rb * nc + c]);
+  }
+  f4 x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = lds4(xs, xidx<0>(c * 32 + i * 4));
+  const float xs8 = 8.f * (xsum[2 * c] + xsum[2 * c + 1]);
+  accA = __builtin_fmaf(da, q4_block_dot(qa, x, xs8), accA);
+  if (two) accB = __builtin_fmaf(db, q4_block_dot(qb, x, xs8), accB);
+}
+
+__device__ __forceinline__ float q8_block_dot(u4 q0, u4 q1, const f4* x, float xs128) {
+  float s = 0.f, t = 0.f;
+  s = dot_ub4(q0.x, x[0], s);
+  t = dot_ub4(q0.y, x[1], t);
+  s = dot_ub4(q0.z, x[2], s);
+  t = dot_ub4(q0.w, x[3], t);
+  s = dot_ub4(q1.x, x[4], s);
+  t = dot_ub4(q1.y, x[5], t);
+  s = dot_ub4(q1.z, x[6], s);
+  t = dot_ub4(q1.w, x[7], t);
+  return (s + t) - xs128;
+}
+
+__device__ __forceinline__ void chunk_q8_0(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
+                                           bool two, const float* xs, const float* xsum, int c,
+                                           float& accA, float& accB) {
+  const size_t nc = A.nchunk;
+  const uint8_t* pa = A.q + (ra * nc + c) * 32;
+  const u4 qa0 = ldg4(pa), qa1 = ldg4(pa + 16);
+  const float da = f16_to_f32(A.d[ra * nc + c]);
+  u4 qb0, qb1;
+  float db = 0.f;
+  if (two) {
+    const uint8_t* pb = B.q + (rb * nc + c) * 32;
+    qb0 = ldg4(pb);
+    qb1 = ldg4(pb + 16);
+    db = f16_to_f32(B.d[rb * nc + c]);
+  }
+  f4 x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = lds4(xs, xidx<0>(c * 32 + i * 4));
+  const float xs128 = 128.f * (xsum[2 * c] + xsum[2 * c + 1]);
+  accA = __builtin_fmaf(da, q8_block_dot(qa0, qa1, x, xs128), accA);
+  if (two) accB = __builtin_fmaf(db, q8_block_dot(qb0, qb1, x, xs128), accB);
+}
+
+// One quarter super-block of Q6_K: byte j of the three planes yields the four
+// 6-bit quants of elements base+j, +32, +64, +96 (src/gguf/dtype.rs:106-115).
+__device__ __forceinline__ float q6_chunk_dot(u4 a, u4 b, u4 h, uint32_t scw, const f4* x,
+                                              const float* xsr) {
+  float r0 = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+  const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+  const uint32_t hv[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t q1 = (av[k] & 0x0F0F0F0Fu) | ((hv[k] & 0x03030303u) << 4);
+    const uint32_t q2 = (bv[k] & 0x0F0F0F0Fu) | ((hv[k] & 0x0C0C0C0Cu) << 2);
+    const uint32_t q3 = ((av[k] >> 4) & 0x0F0F0F0Fu) | (hv[k] & 0x30303030u);
+    const uint32_t q4 = ((bv[k] >> 4) & 0x0F0F0F0Fu) | ((hv[k] & 0xC0C0C0C0u) >> 2);
+    r0 = dot_ub4(q1, x[k], r0);
+    r1 = dot_ub4(q2, x[4 + k], r1);
+    r2 = dot_ub4(q3, x[8 + k], r2);
+    r3 = dot_ub4(q4, x[12 + k], r3);
+  }
+  const float s0 = (float)(int8_t)(scw & 0xFF), s1 = (float)(int8_t)((scw >> 8) & 0xFF);
+  const float s2 = (float)(int8_t)((scw >> 16) & 0xFF), s3 = (float)(int8_t)(scw >> 24);
+  float t = s0 * (r0 - xsr[0]);
+  t = __builtin_fmaf(s1, r1 - xsr[1], t);
+  t = __builtin_fmaf(s2, r2 - xsr[2], t);
+  t = __builtin_fmaf(s3, r3 - xsr[3], t);
+  return t;
+}
+
+__device__ __forceinline__ void chunk_q6_k(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
+                                           bool two, const float* xs, const float* xsum, int c,
+                                           float& accA, float& accB) {
+  const size_t nc = A.nchunk;
+  const uint8_t* pa = A.q + ra * nc * 48 + (size_t)c * 16;
+  const u4 a0 = ldg4(pa), a1 = ldg4(pa + nc * 16), a2 = ldg4(pa + nc * 32);
+  const uint32_t sca = A.sc[ra * nc + c];
+  const float da = f16_to_f32(A.d[ra * (nc >> 2) + (c >> 2)]);
+  u4 b0, b1, b2;
+  uint32_t scb = 0;
+  float db = 0.f;
+  if (two) {
+    const uint8_t* pb = B.q + rb * nc * 48 + (size_t)c * 16;
+    b0 = ldg4(pb);
+    b1 = ldg4(pb + nc * 16);
+    b2 = ldg4(pb + nc * 32);
+    scb = B.sc[rb * nc + c];
+    db = f16_to_f32(B.d[rb * (nc >> 2) + (c >> 2)]);
+  }
+  const int base = (c >> 2) * 256 + ((c >> 1) & 1) * 128 + (c & 1) * 16;
+  f4 x[16];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[r * 4 + k] = lds4(xs, xidx<1>(base + r * 32 + k * 4));
+  float xsr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xsr[r] = 32.f * xsum[(base + r * 32) >> 4];
+  accA = __builtin_fmaf(da, q6_chunk_dot(a0, a1, a2, sca, x, xsr), accA);
+  if (two) accB = __builtin_fmaf(db, q6_chunk_dot(b0, b1, b2, scb, x, xsr), accB);
+}
+
+// Stage n floats of x into LDS (layouts flagged by need0/need1) plus the
+// per-16 group sums, zero-padded up to a multiple of 16.  With `norm`, x is
+// replaced by rmsnorm(x)*w as in src/math/ops.rs:5-12:
+// x[i] * (1/sqrt(sum(x^2)/n + eps)) * w[i].  blockDim.x must be 256; x and w
+// must be 16-byte aligned.  Ends with __syncthreads().
+__device__ __forceinline__ f4 load_x4(const float* __restrict__ p, int e, int n) {
+  if (e + 3 < n) return *reinterpret_cast<const f4*>(p + e);
+  f4 v = {0.f, 0.f, 0.f, 0.f};
+  if (e < n) v.x = p[e];
+  if (e + 1 < n) v.y = p[e + 1];
+  if (e + 2 < n) v.z = p[e + 2];
+  return v;
+}
+
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int n, const float* __restrict__ w,
+                                        float eps, bool norm, float* xs0, float* xs1, float* xsum,
+                                        float* red, bool need0, bool need1) {
+  const int tid = threadIdx.x;
+  const int npad = (n + 15) & ~15;
+  float scale = 1.f;
+  if (norm) {
+    float ss = 0.f;
+    for (int i = tid * 4; i < npad; i += 256 * 4) {
+      const f4 v = load_x4(x, i, n);
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = block_sum(ss, red, 4);
+    scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+  // Every group of four consecutive threads holds one complete 16-element
+  // group for the xsum shuffle.
+  const int n4 = npad >> 2;
+  const int iters = (n4 + 255) >> 8;
+  for (int it = 0; it < iters; ++it) {
+    const int e4 = it * 256 + tid;
+    f4 v = {0.f, 0.f, 0.f, 0.f};
+    if (e4 < n4) {
+      v = load_x4(x, e4 * 4, n);
+      if (norm) {
+        const f4 ww = load_x4(w, e4 * 4, n);
+        v.x = v.x * scale * ww.x;
+        v.y = v.y * scale * ww.y;
+        v.z = v.z * scale * ww.z;
+        v.w = v.w * scale * ww.w;
+      }
+      if (need0) *reinterpret_cast<f4*>(xs0 + xidx<0>(e4 * 4)) = v;
+      if (need1) *reinterpret_cast<f4*>(xs1 + xidx<1>(e4 * 4)) = v;
+    }
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += __shfl_xor(s, 1, TALOS_WAVE);
+    s += __shfl_xor(s, 2, TALOS_WAVE);
+    if (e4 < n4 && (tid & 3) == 0) xsum[e4 >> 2] = s;
+  }
+  __syncthreads();
+}

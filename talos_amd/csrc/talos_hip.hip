@@ -1,0 +1,798 @@
+// talos_hip.hip -- MI355X decode backend behind the C ABI in include/talos_hip.h.
+//
+// Host orchestration for the reference's GPU forward (Tsuskov/talos
+// src/math/metal/mod.rs:368-520), re-designed for gfx950:
+//  * weights are repacked once at upload (layout.h) and stay resident in HBM,
+//    keyed by tensor name;
+//  * the K/V cache, residual stream and activations stay on the device;
+//  * a token step is ~5 kernels per layer (kernels.h) captured once into a
+//    hipGraph whose position/token come from device memory, so every step is
+//    one graph launch plus the logits read-back.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/talos_hip.h"
+#include "kernels.h"
+
+namespace {
+
+std::string g_create_error;
+
+struct DevWeight {
+  uint32_t type = 0;
+  size_t rows = 0, cols = 0, len = 0;
+  void* mem = nullptr;
+  DevMat mat{};
+  const float* f32 = nullptr;  // F32 tensors: the plain row-major data
+};
+
+enum GraphKind { G_LOGITS = 0, G_HIDDEN = 1, G_TOKEN = 2, G_GREEDY = 3, G_COUNT = 4 };
+
+}  // namespace
+
+struct talos_hip_ctx {
+  talos_hip_cfg cfg{};
+  uint32_t hd = 0, kv_dim = 0, group = 0, nsplit = 1, max_chunk = 1;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::unordered_map<std::string, DevWeight> weights;
+  size_t max_lds = 0;
+
+  // device buffers
+  bool acts_ready = false;
+  std::vector<float*> kc, vc;
+  int32_t* io = nullptr;  // [state: 16 int32][x: n_embd floats]
+  float* x = nullptr;     // = io + 16
+  float* q = nullptr;
+  float* atty = nullptr;
+  float* h = nullptr;
+  float* logits = nullptr;
+  float* hidden = nullptr;
+  float* part = nullptr;
+  uint32_t* count = nullptr;
+  int32_t* tokens = nullptr;
+  float* rope = nullptr;
+  float* mv_x = nullptr;  // standalone matvec staging
+  float* mv_out = nullptr;
+  size_t mv_x_cap = 0, mv_out_cap = 0;
+
+  // pinned host staging
+  int32_t* h_io = nullptr;
+  float* h_out = nullptr;
+  int32_t* h_tokens = nullptr;
+
+  hipGraphExec_t graph[G_COUNT] = {nullptr, nullptr, nullptr, nullptr};
+};
+
+namespace {
+
+int fail(talos_hip_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  else g_create_error = buf;
+  return code;
+}
+
+#define HIPCHK(c, call)                                                                         \
+  do {                                                                                          \
+    hipError_t e_ = (call);                                                                     \
+    if (e_ != hipSuccess)                                                                       \
+      return fail((c), TALOS_ERR_HIP, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_),    \
+                  __FILE__, __LINE__);                                                          \
+  } while (0)
+
+size_t block_elems(uint32_t t) { return t == TALOS_GGML_F32 ? 1 : t == TALOS_GGML_Q6_K ? 256 : 32; }
+size_t block_bytes(uint32_t t) {
+  return t == TALOS_GGML_F32 ? 4 : t == TALOS_GGML_Q8_0 ? 34 : t == TALOS_GGML_Q4_0 ? 18 : 210;
+}
+bool type_ok(uint32_t t) {
+  return t == TALOS_GGML_F32 || t == TALOS_GGML_Q8_0 || t == TALOS_GGML_Q4_0 || t == TALOS_GGML_Q6_K;
+}
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+void destroy_graphs(talos_hip_ctx* c) {
+  for (auto& g : c->graph)
+    if (g) {
+      (void)hipGraphExecDestroy(g);
+      g = nullptr;
+    }
+}
+
+// Repack GGUF blocks into the device layout of layout.h; returns the host
+// image and the plane offsets.
+struct Packed {
+  std::vector<uint8_t> img;
+  size_t q_off = 0, sc_off = 0, d_off = 0;
+  uint32_t nchunk = 0;
+};
+
+void repack(const uint8_t* src, uint32_t type, size_t rows, size_t cols, Packed& P) {
+  if (type == TALOS_GGML_F32) {  // rows zero-padded to a multiple of 16 floats
+    const size_t ld = (cols + 15) & ~size_t(15);
+    P.img.assign(rows * ld * 4, 0);
+    for (size_t r = 0; r < rows; ++r) memcpy(P.img.data() + r * ld * 4, src + r * cols * 4, cols * 4);
+    P.nchunk = (uint32_t)(ld / 4);
+    return;
+  }
+  if (type == TALOS_GGML_Q8_0 || type == TALOS_GGML_Q4_0) {
+    const size_t nb = cols / 32, bb = block_bytes(type), qb = type == TALOS_GGML_Q8_0 ? 32 : 16;
+    P.nchunk = (uint32_t)nb;
+    P.q_off = 0;
+    P.d_off = align256(rows * nb * qb);
+    P.img.assign(P.d_off + align256(rows * nb * 2), 0);
+    uint8_t* q = P.img.data();
+    uint16_t* d = reinterpret_cast<uint16_t*>(P.img.data() + P.d_off);
+    for (size_t b = 0; b < rows * nb; ++b) {
+      const uint8_t* s = src + b * bb;
+      d[b] = (uint16_t)(s[0] | (s[1] << 8));
+      if (type == TALOS_GGML_Q8_0) {
+        for (int j = 0; j < 32; ++j) q[b * 32 + j] = s[2 + j] ^ 0x80;
+      } else {
+        memcpy(q + b * 16, s + 2, 16);
+      }
+    }
+    return;
+  }
+  // Q6_K: super-block = ql[128] qh[64] sc[16] d(f16) (src/gguf/dtype.rs:94-102)
+  const size_t nsb = cols / 256, nc = nsb * 4;
+  P.nchunk = (uint32_t)nc;
+  P.q_off = 0;
+  P.sc_off = align256(rows * nc * 48);
+  P.d_off = P.sc_off + align256(rows * nc * 4);
+  P.img.assign(P.d_off + align256(rows * nsb * 2), 0);
+  uint8_t* q = P.img.data();
+  uint32_t* scw = reinterpret_cast<uint32_t*>(P.img.data() + P.sc_off);
+  uint16_t* d = reinterpret_cast<uint16_t*>(P.img.data() + P.d_off);
+  for (size_t r = 0; r < rows; ++r) {
+    uint8_t* qrow = q + r * nc * 48;
+    for (size_t sb = 0; sb < nsb; ++sb) {
+      const uint8_t* s = src + (r * nsb + sb) * 210;
+      const uint8_t *ql = s, *qh = s + 128, *sc = s + 192;
+      d[r * nsb + sb] = (uint16_t)(s[208] | (s[209] << 8));
+      for (int n = 0; n < 2; ++n)
+        for (int g = 0; g < 2; ++g) {
+          const size_t c = sb * 4 + n * 2 + g;
+          memcpy(qrow + 0 * nc * 16 + c * 16, ql + n * 64 + g * 16, 16);
+          memcpy(qrow + 1 * nc * 16 + c * 16, ql + n * 64 + 32 + g * 16, 16);
+          memcpy(qrow + 2 * nc * 16 + c * 16, qh + n * 32 + g * 16, 16);
+          const int is = n * 8 + g;
+          scw[r * nc + c] = (uint32_t)sc[is] | ((uint32_t)sc[is + 2] << 8) | ((uint32_t)sc[is + 4] << 16) |
+                            ((uint32_t)sc[is + 6] << 24);
+        }
+    }
+  }
+}
+
+const DevWeight* find_w(talos_hip_ctx* c, const std::string& name) {
+  auto it = c->weights.find(name);
+  return it == c->weights.end() ? nullptr : &it->second;
+}
+
+int need_matrix(talos_hip_ctx* c, const std::string& name, size_t rows, size_t cols, const DevWeight** out) {
+  const DevWeight* w = find_w(c, name);
+  if (!w) return fail(c, TALOS_ERR_MISSING_WEIGHT, "weight \"%s\" is not resident", name.c_str());
+  if (w->rows != rows || w->cols != cols)
+    return fail(c, TALOS_ERR_SHAPE, "weight \"%s\" is [%zu, %zu], the model needs [%zu, %zu]", name.c_str(),
+                w->rows, w->cols, rows, cols);
+  *out = w;
+  return TALOS_OK;
+}
+
+int need_norm(talos_hip_ctx* c, const std::string& name, size_t n, const float** out) {
+  const DevWeight* w = find_w(c, name);
+  if (!w) return fail(c, TALOS_ERR_MISSING_WEIGHT, "weight \"%s\" is not resident", name.c_str());
+  if (w->type != TALOS_GGML_F32 || w->rows * w->cols != n)
+    return fail(c, TALOS_ERR_SHAPE, "norm \"%s\" must be F32 with %zu elements", name.c_str(), n);
+  *out = w->f32;
+  return TALOS_OK;
+}
+
+int layout_need(uint32_t fmt) { return 1 << fmt_xlayout(fmt); }
+
+void plan(uint32_t units, uint32_t& upw, uint32_t& blocks) {
+  const uint32_t max_waves = 2048 * 4;
+  upw = (units + max_waves - 1) / max_waves;
+  if (upw == 0) upw = 1;
+  const uint32_t waves = (units + upw - 1) / upw;
+  blocks = (waves + 3) / 4;
+  if (blocks == 0) blocks = 1;
+}
+
+int alloc_acts(talos_hip_ctx* c) {
+  if (c->acts_ready) return TALOS_OK;
+  const auto& cf = c->cfg;
+  const size_t kvb = (size_t)cf.context_length * c->kv_dim * 4;
+  c->kc.assign(cf.n_layer, nullptr);
+  c->vc.assign(cf.n_layer, nullptr);
+  for (uint32_t l = 0; l < cf.n_layer; ++l) {
+    HIPCHK(c, hipMalloc(&c->kc[l], kvb));
+    HIPCHK(c, hipMalloc(&c->vc[l], kvb));
+    HIPCHK(c, hipMemsetAsync(c->kc[l], 0, kvb, c->stream));
+    HIPCHK(c, hipMemsetAsync(c->vc[l], 0, kvb, c->stream));
+  }
+  HIPCHK(c, hipMalloc(&c->io, 64 + (size_t)cf.n_embd * 4));
+  HIPCHK(c, hipMemsetAsync(c->io, 0, 64 + (size_t)cf.n_embd * 4, c->stream));
+  c->x = reinterpret_cast<float*>(c->io + 16);
+  HIPCHK(c, hipMalloc(&c->q, (size_t)cf.n_embd * 4));
+  HIPCHK(c, hipMalloc(&c->atty, (size_t)cf.n_embd * 4));
+  HIPCHK(c, hipMalloc(&c->h, (size_t)cf.n_ff * 4));
+  HIPCHK(c, hipMalloc(&c->logits, (size_t)cf.vocab_size * 4));
+  HIPCHK(c, hipMalloc(&c->hidden, (size_t)cf.n_embd * 4));
+  const size_t part_n = (size_t)cf.n_head_kv * c->nsplit * c->group * (c->hd + 2);
+  HIPCHK(c, hipMalloc(&c->part, part_n * 4));
+  HIPCHK(c, hipMalloc(&c->count, (size_t)cf.n_head_kv * 4));
+  HIPCHK(c, hipMemsetAsync(c->count, 0, (size_t)cf.n_head_kv * 4, c->stream));
+  HIPCHK(c, hipMalloc(&c->tokens, (size_t)cf.context_length * 4));
+  HIPCHK(c, hipHostMalloc(&c->h_io, 64 + (size_t)cf.n_embd * 4, hipHostMallocDefault));
+  HIPCHK(c, hipHostMalloc(&c->h_out, (size_t)std::max(cf.vocab_size, cf.n_embd) * 4, hipHostMallocDefault));
+  HIPCHK(c, hipHostMalloc(&c->h_tokens, (size_t)cf.context_length * 4, hipHostMallocDefault));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  c->acts_ready = true;
+  return TALOS_OK;
+}
+
+// ---- per-kernel enqueue (shared by graph capture and kernel timing)
+
+struct LayerW {
+  const DevWeight *q, *k, *v, *o, *g, *u, *d;
+  const float *an, *fn;
+};
+
+int layer_weights(talos_hip_ctx* c, uint32_t l, LayerW* w) {
+  const auto& cf = c->cfg;
+  const uint32_t n = cf.n_embd, kvd = c->kv_dim;
+  char nm[128];
+  int rc;
+#define NM(s) (snprintf(nm, sizeof nm, "blk.%u." s, l), std::string(nm))
+  if ((rc = need_norm(c, NM("attn_norm.weight"), n, &w->an)) || (rc = need_matrix(c, NM("attn_q.weight"), n, n, &w->q)) ||
+      (rc = need_matrix(c, NM("attn_k.weight"), kvd, n, &w->k)) ||
+      (rc = need_matrix(c, NM("attn_v.weight"), kvd, n, &w->v)) ||
+      (rc = need_matrix(c, NM("attn_output.weight"), n, n, &w->o)) ||
+      (rc = need_norm(c, NM("ffn_norm.weight"), n, &w->fn)) ||
+      (rc = need_matrix(c, NM("ffn_gate.weight"), cf.n_ff, n, &w->g)) ||
+      (rc = need_matrix(c, NM("ffn_up.weight"), cf.n_ff, n, &w->u)) ||
+      (rc = need_matrix(c, NM("ffn_down.weight"), n, cf.n_ff, &w->d)))
+    return rc;
+#undef NM
+  return TALOS_OK;
+}
+
+void enq_qkv(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
+  const uint32_t n = c->cfg.n_embd, kvd = c->kv_dim;
+  QKVParams P{};
+  P.m[0] = w.q->mat;
+  P.m[1] = w.k->mat;
+  P.m[2] = w.v->mat;
+  P.units[0] = n / 2;
+  P.units[1] = kvd / 2;
+  P.units[2] = kvd / 2;
+  P.x = c->x;
+  P.norm_w = w.an;
+  P.eps = c->cfg.rms_eps;
+  P.n = n;
+  P.q_out = c->q;
+  P.kc = c->kc[l];
+  P.vc = c->vc[l];
+  P.kv_dim = kvd;
+  P.hd = c->hd;
+  P.rope = c->rope;
+  P.state = c->io;
+  P.need = layout_need(w.q->mat.fmt) | layout_need(w.k->mat.fmt) | layout_need(w.v->mat.fmt);
+  uint32_t blocks;
+  plan(P.units[0] + P.units[1] + P.units[2], P.upw, blocks);
+  hipLaunchKernelGGL(k_qkv, dim3(blocks), dim3(256), stage_lds_bytes(n, P.need), c->stream, P);
+}
+
+void enq_attn(talos_hip_ctx* c, uint32_t l) {
+  AttnParams A{};
+  A.q = c->q;
+  A.kc = c->kc[l];
+  A.vc = c->vc[l];
+  A.out = c->atty;
+  A.part = c->part;
+  A.count = c->count;
+  A.state = c->io;
+  A.hd = c->hd;
+  A.kv_dim = c->kv_dim;
+  A.group = c->group;
+  A.nsplit = c->nsplit;
+  A.max_chunk = c->max_chunk;
+  A.scale = 1.0f / sqrtf((float)c->hd);
+  const dim3 grid(c->cfg.n_head_kv, c->nsplit);
+  const size_t lds = attn_lds_bytes(c->hd, c->group, c->max_chunk);
+  switch (c->hd / 16) {
+    case 2: hipLaunchKernelGGL(k_attn<2>, grid, dim3(256), lds, c->stream, A); break;
+    case 3: hipLaunchKernelGGL(k_attn<3>, grid, dim3(256), lds, c->stream, A); break;
+    case 4: hipLaunchKernelGGL(k_attn<4>, grid, dim3(256), lds, c->stream, A); break;
+    case 5: hipLaunchKernelGGL(k_attn<5>, grid, dim3(256), lds, c->stream, A); break;
+    case 6: hipLaunchKernelGGL(k_attn<6>, grid, dim3(256), lds, c->stream, A); break;
+    case 7: hipLaunchKernelGGL(k_attn<7>, grid, dim3(256), lds, c->stream, A); break;
+    default: hipLaunchKernelGGL(k_attn<8>, grid, dim3(256), lds, c->stream, A); break;
+  }
+}
+
+void enq_resid(talos_hip_ctx* c, const DevWeight* w, const float* x, uint32_t n, float* out) {
+  RowParams R{};
+  R.m = w->mat;
+  R.x = x;
+  R.n = n;
+  R.out = out;
+  R.accumulate = 1;
+  R.units = (uint32_t)((w->rows + 1) / 2);
+  R.need = layout_need(w->mat.fmt);
+  uint32_t blocks;
+  plan(R.units, R.upw, blocks);
+  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), stage_lds_bytes(n, R.need), c->stream, R);
+}
+
+void enq_gateup(talos_hip_ctx* c, const LayerW& w) {
+  GateUpParams G{};
+  G.g = w.g->mat;
+  G.u = w.u->mat;
+  G.x = c->x;
+  G.norm_w = w.fn;
+  G.eps = c->cfg.rms_eps;
+  G.n = c->cfg.n_embd;
+  G.h = c->h;
+  G.units = c->cfg.n_ff;
+  G.need = layout_need(w.g->mat.fmt) | layout_need(w.u->mat.fmt);
+  uint32_t blocks;
+  plan(G.units, G.upw, blocks);
+  hipLaunchKernelGGL(k_gateup, dim3(blocks), dim3(256), stage_lds_bytes(G.n, G.need), c->stream, G);
+}
+
+void enq_output(talos_hip_ctx* c, const DevWeight* wout, const float* onorm) {
+  RowParams R{};
+  R.m = wout->mat;
+  R.x = c->x;
+  R.norm_w = onorm;
+  R.eps = c->cfg.rms_eps;
+  R.n = c->cfg.n_embd;
+  R.out = c->logits;
+  R.accumulate = 0;
+  R.units = (c->cfg.vocab_size + 1) / 2;
+  R.need = layout_need(wout->mat.fmt);
+  uint32_t blocks;
+  plan(R.units, R.upw, blocks);
+  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), stage_lds_bytes(R.n, R.need), c->stream, R);
+}
+
+// Enqueue one token step on the stream.
+int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
+  const auto& cf = c->cfg;
+  const uint32_t n = cf.n_embd;
+  int rc;
+  if (kind == G_TOKEN || kind == G_GREEDY) {
+    const DevWeight* emb;
+    if ((rc = need_matrix(c, "token_embd.weight", cf.vocab_size, n, &emb))) return rc;
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, c->stream, emb->mat, (const int32_t*)c->io, c->x);
+  }
+  for (uint32_t l = 0; l < cf.n_layer; ++l) {
+    LayerW w;
+    if ((rc = layer_weights(c, l, &w))) return rc;
+    enq_qkv(c, l, w);
+    enq_attn(c, l);
+    enq_resid(c, w.o, c->atty, n, c->x);
+    enq_gateup(c, w);
+    enq_resid(c, w.d, c->h, cf.n_ff, c->x);
+  }
+  const float* onorm;
+  if ((rc = need_norm(c, "output_norm.weight", n, &onorm))) return rc;
+  if (kind == G_HIDDEN) {
+    hipLaunchKernelGGL(k_norm, dim3(1), dim3(256), 0, c->stream, c->x, onorm, cf.rms_eps, n, c->hidden);
+    return TALOS_OK;
+  }
+  const DevWeight* wout;
+  if ((rc = need_matrix(c, "output.weight", cf.vocab_size, n, &wout))) return rc;
+  enq_output(c, wout, onorm);
+  if (kind == G_TOKEN || kind == G_GREEDY)
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, c->stream, c->logits, cf.vocab_size, c->io, c->tokens,
+                       kind == G_GREEDY ? 1 : 0);
+  return TALOS_OK;
+}
+
+int get_graph(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t* out) {
+  int rc;
+  if ((rc = alloc_acts(c))) return rc;
+  if (c->graph[kind]) {
+    *out = c->graph[kind];
+    return TALOS_OK;
+  }
+  hipGraph_t g = nullptr;
+  HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  rc = enqueue_token(c, kind);
+  hipError_t e = hipStreamEndCapture(c->stream, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return fail(c, TALOS_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(&c->graph[kind], g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(c, TALOS_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  *out = c->graph[kind];
+  return TALOS_OK;
+}
+
+int set_state(talos_hip_ctx* c, uint32_t token, uint32_t pos);
+
+int check_ctx(talos_hip_ctx* c) {
+  if (!c) return TALOS_ERR_ARG;
+  c->err.clear();
+  return TALOS_OK;
+}
+
+int set_device(talos_hip_ctx* c) {
+  HIPCHK(c, hipSetDevice(c->cfg.device));
+  return TALOS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
+  g_create_error.clear();
+  if (!cfg || !out) return fail(nullptr, TALOS_ERR_ARG, "null cfg or out");
+  *out = nullptr;
+  const talos_hip_cfg& f = *cfg;
+  if (!f.n_layer || !f.n_head || !f.n_head_kv || !f.n_embd || !f.n_ff || !f.vocab_size || !f.context_length)
+    return fail(nullptr, TALOS_ERR_ARG, "config has a zero dimension");
+  if (f.n_head % f.n_head_kv != 0)
+    return fail(nullptr, TALOS_ERR_ARG, "head_count %u must be a positive multiple of head_count_kv %u", f.n_head,
+                f.n_head_kv);
+  if (f.n_embd % f.n_head != 0) return fail(nullptr, TALOS_ERR_ARG, "n_embd %u not divisible by n_head", f.n_embd);
+  const uint32_t hd = f.n_embd / f.n_head;
+  if (hd % 16 != 0 || hd < 32 || hd > 128)
+    return fail(nullptr, TALOS_ERR_ARG, "head_dim %u unsupported (needs a multiple of 16 in [32, 128])", hd);
+  if (f.n_head / f.n_head_kv > TALOS_MAX_GROUP)
+    return fail(nullptr, TALOS_ERR_ARG, "GQA group %u exceeds %d", f.n_head / f.n_head_kv, TALOS_MAX_GROUP);
+  if (f.n_embd % 4 != 0 || f.n_ff % 4 != 0)
+    return fail(nullptr, TALOS_ERR_ARG, "n_embd and n_ff must be multiples of 4");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
+    return fail(nullptr, TALOS_ERR_HIP, "no HIP device available");
+  if (f.device < 0 || f.device >= ndev) return fail(nullptr, TALOS_ERR_ARG, "device %d out of range", f.device);
+
+  auto c = std::make_unique<talos_hip_ctx>();
+  c->cfg = f;
+  c->hd = hd;
+  c->kv_dim = f.n_head_kv * hd;
+  c->group = f.n_head / f.n_head_kv;
+  uint32_t ns = (f.context_length + 127) / 128;
+  c->nsplit = ns < 1 ? 1 : (ns > 64 ? 64 : ns);
+  c->max_chunk = (f.context_length + c->nsplit - 1) / c->nsplit;
+  hipError_t e = hipSetDevice(f.device);
+  if (e != hipSuccess) return fail(nullptr, TALOS_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, f.device)) != hipSuccess)
+    return fail(nullptr, TALOS_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  c->max_lds = prop.sharedMemPerBlock;
+  const size_t need_lds = stage_lds_bytes((int)std::max(f.n_embd, f.n_ff), 3);
+  if (need_lds > c->max_lds)
+    return fail(nullptr, TALOS_ERR_ARG, "n_ff %u needs %zu B of LDS, device has %zu", f.n_ff, need_lds, c->max_lds);
+  for (const void* k : {(const void*)k_qkv, (const void*)k_rows, (const void*)k_gateup})
+    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+  if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
+    return fail(nullptr, TALOS_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+
+  // RoPE table, same expression as src/math/ops.rs:48-61 evaluated in f32
+  // with the C library's powf/sinf/cosf.
+  const uint32_t half = hd / 2;
+  std::vector<float> rope((size_t)f.context_length * half * 2);
+  for (uint32_t p = 0; p < f.context_length; ++p)
+    for (uint32_t i = 0; i < half; ++i) {
+      const float expo = (-2.0f * (float)i) / (float)hd;
+      const float theta = (float)p * powf(f.rope_freq_base, expo);
+      rope[((size_t)p * half + i) * 2 + 0] = cosf(theta);
+      rope[((size_t)p * half + i) * 2 + 1] = sinf(theta);
+    }
+  if ((e = hipMalloc(&c->rope, rope.size() * 4)) != hipSuccess ||
+      (e = hipMemcpy(c->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) {
+    talos_hip_destroy(c.release());
+    return fail(nullptr, TALOS_ERR_HIP, "rope table: %s", hipGetErrorString(e));
+  }
+  *out = c.release();
+  return TALOS_OK;
+}
+
+void talos_hip_destroy(talos_hip_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->cfg.device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  destroy_graphs(c);
+  for (auto& kv : c->weights) (void)hipFree(kv.second.mem);
+  for (float* p : c->kc) (void)hipFree(p);
+  for (float* p : c->vc) (void)hipFree(p);
+  void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope, c->mv_x, c->mv_out};
+  for (void* p : dev)
+    if (p) (void)hipFree(p);
+  if (c->h_io) (void)hipHostFree(c->h_io);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->h_tokens) (void)hipHostFree(c->h_tokens);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* talos_hip_last_error(const talos_hip_ctx* c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+int talos_hip_upload_weight(talos_hip_ctx* c, const char* name, const void* bytes, size_t len, uint32_t type,
+                            size_t rows, size_t cols) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!name || !bytes) return fail(c, TALOS_ERR_ARG, "null name or bytes");
+  if (!type_ok(type)) return fail(c, TALOS_ERR_DTYPE, "tensor \"%s\" has unsupported ggml type %u", name, type);
+  if (!rows || !cols) return fail(c, TALOS_ERR_SHAPE, "tensor \"%s\" has an empty shape", name);
+  const size_t be = block_elems(type);
+  if (cols % be) return fail(c, TALOS_ERR_SHAPE, "tensor \"%s\": cols %zu not a multiple of block %zu", name, cols, be);
+  const size_t want = rows * (cols / be) * block_bytes(type);
+  if (len != want)
+    return fail(c, TALOS_ERR_SHAPE, "tensor \"%s\": %zu bytes, [%zu, %zu] of type %u needs %zu", name, len, rows, cols,
+                type, want);
+  auto it = c->weights.find(name);
+  if (it != c->weights.end() && it->second.len == len) return TALOS_OK;  // resident (metal/mod.rs:64-68)
+  if ((rc = set_device(c))) return rc;
+  Packed P;
+  repack(static_cast<const uint8_t*>(bytes), type, rows, cols, P);
+  DevWeight w;
+  w.type = type;
+  w.rows = rows;
+  w.cols = cols;
+  w.len = len;
+  HIPCHK(c, hipMalloc(&w.mem, P.img.size()));
+  hipError_t e = hipMemcpy(w.mem, P.img.data(), P.img.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(w.mem);
+    return fail(c, TALOS_ERR_HIP, "upload of \"%s\": %s", name, hipGetErrorString(e));
+  }
+  uint8_t* base = static_cast<uint8_t*>(w.mem);
+  w.mat.q = base + P.q_off;
+  w.mat.d = type == TALOS_GGML_F32 ? nullptr : reinterpret_cast<const uint16_t*>(base + P.d_off);
+  w.mat.sc = type == TALOS_GGML_Q6_K ? reinterpret_cast<const uint32_t*>(base + P.sc_off) : nullptr;
+  w.mat.rows = (uint32_t)rows;
+  w.mat.cols = (uint32_t)cols;
+  w.mat.fmt = type;
+  w.mat.nchunk = P.nchunk;
+  w.f32 = type == TALOS_GGML_F32 ? reinterpret_cast<const float*>(base) : nullptr;
+  if (it != c->weights.end()) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(it->second.mem);
+    it->second = w;
+  } else {
+    c->weights.emplace(name, w);
+  }
+  destroy_graphs(c);  // graphs captured the old pointers
+  return TALOS_OK;
+}
+
+static int forward_host(talos_hip_ctx* c, const float* x_embed, uint32_t pos, float* out, GraphKind kind) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!x_embed || !out) return fail(c, TALOS_ERR_ARG, "null x_embed or output");
+  if (pos >= c->cfg.context_length)
+    return fail(c, TALOS_ERR_POS, "pos %u >= context_length %u", pos, c->cfg.context_length);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, kind, &g))) return rc;
+  const uint32_t n = c->cfg.n_embd;
+  memset(c->h_io, 0, 64);
+  c->h_io[ST_POS] = (int32_t)pos;
+  memcpy(c->h_io + 16, x_embed, (size_t)n * 4);
+  HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64 + (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, hipGraphLaunch(g, c->stream));
+  const size_t out_n = kind == G_HIDDEN ? n : c->cfg.vocab_size;
+  HIPCHK(c, hipMemcpyAsync(c->h_out, kind == G_HIDDEN ? c->hidden : c->logits, out_n * 4, hipMemcpyDeviceToHost,
+                           c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  memcpy(out, c->h_out, out_n * 4);
+  return TALOS_OK;
+}
+
+int talos_hip_forward(talos_hip_ctx* c, const float* x_embed, uint32_t pos, float* logits) {
+  return forward_host(c, x_embed, pos, logits, G_LOGITS);
+}
+
+int talos_hip_forward_hidden(talos_hip_ctx* c, const float* x_embed, uint32_t pos, float* hidden) {
+  return forward_host(c, x_embed, pos, hidden, G_HIDDEN);
+}
+
+namespace {
+int set_state(talos_hip_ctx* c, uint32_t token, uint32_t pos) {
+  memset(c->h_io, 0, 64);
+  c->h_io[ST_POS] = (int32_t)pos;
+  c->h_io[ST_TOKEN] = (int32_t)token;
+  c->h_io[ST_STEP] = 0;
+  HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64, hipMemcpyHostToDevice, c->stream));
+  return TALOS_OK;
+}
+}  // namespace
+
+int talos_hip_forward_token(talos_hip_ctx* c, uint32_t token, uint32_t pos, float* logits, uint32_t* argmax) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (pos >= c->cfg.context_length)
+    return fail(c, TALOS_ERR_POS, "pos %u >= context_length %u", pos, c->cfg.context_length);
+  if (token >= c->cfg.vocab_size)
+    return fail(c, TALOS_ERR_TOKEN, "token %u >= vocab_size %u", token, c->cfg.vocab_size);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_TOKEN, &g))) return rc;
+  if ((rc = set_state(c, token, pos))) return rc;
+  HIPCHK(c, hipGraphLaunch(g, c->stream));
+  if (logits)
+    HIPCHK(c, hipMemcpyAsync(c->h_out, c->logits, (size_t)c->cfg.vocab_size * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if (logits) memcpy(logits, c->h_out, (size_t)c->cfg.vocab_size * 4);
+  if (argmax) *argmax = (uint32_t)c->h_io[ST_ARGMAX];
+  return TALOS_OK;
+}
+
+int talos_hip_decode_greedy(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint32_t n_steps, uint32_t* tokens_out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!tokens_out && n_steps) return fail(c, TALOS_ERR_ARG, "null tokens_out");
+  if ((uint64_t)pos + n_steps > c->cfg.context_length)
+    return fail(c, TALOS_ERR_POS, "pos %u + %u steps exceeds context_length %u", pos, n_steps, c->cfg.context_length);
+  if (token >= c->cfg.vocab_size)
+    return fail(c, TALOS_ERR_TOKEN, "token %u >= vocab_size %u", token, c->cfg.vocab_size);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_GREEDY, &g))) return rc;
+  if ((rc = set_state(c, token, pos))) return rc;
+  for (uint32_t s = 0; s < n_steps; ++s) HIPCHK(c, hipGraphLaunch(g, c->stream));
+  if (n_steps)
+    HIPCHK(c, hipMemcpyAsync(c->h_tokens, c->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  for (uint32_t s = 0; s < n_steps; ++s) tokens_out[s] = (uint32_t)c->h_tokens[s];
+  return TALOS_OK;
+}
+
+int talos_hip_kv_reset(talos_hip_ctx* c) { return check_ctx(c); }
+
+int talos_hip_kv_read(talos_hip_ctx* c, uint32_t n_pos, float* k_out, float* v_out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!k_out || !v_out) return fail(c, TALOS_ERR_ARG, "null output");
+  if (n_pos > c->cfg.context_length) return fail(c, TALOS_ERR_POS, "n_pos %u > context_length", n_pos);
+  if ((rc = set_device(c))) return rc;
+  if ((rc = alloc_acts(c))) return rc;
+  const size_t row = (size_t)n_pos * c->kv_dim;
+  for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
+    HIPCHK(c, hipMemcpyAsync(k_out + l * row, c->kc[l], row * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(v_out + l * row, c->vc[l], row * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return TALOS_OK;
+}
+
+static int enqueue_matvec(talos_hip_ctx* c, const DevWeight* w, const float* d_x, float* d_out) {
+  RowParams R{};
+  R.m = w->mat;
+  R.x = d_x;
+  R.n = (uint32_t)w->cols;
+  R.out = d_out;
+  R.accumulate = 0;
+  R.units = (uint32_t)((w->rows + 1) / 2);
+  R.need = layout_need(w->mat.fmt);
+  const size_t lds = stage_lds_bytes((int)w->cols, R.need);
+  if (lds > c->max_lds) return fail(c, TALOS_ERR_SHAPE, "cols %zu needs %zu B of LDS", w->cols, lds);
+  uint32_t blocks;
+  plan(R.units, R.upw, blocks);
+  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), lds, c->stream, R);
+  HIPCHK(c, hipGetLastError());
+  return TALOS_OK;
+}
+
+int talos_hip_matvec(talos_hip_ctx* c, const char* name, const void* bytes, size_t len, uint32_t type, size_t rows,
+                     size_t cols, const float* x, float* out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!x || !out) return fail(c, TALOS_ERR_ARG, "null x or out");
+  if ((rc = talos_hip_upload_weight(c, name, bytes, len, type, rows, cols))) return rc;
+  const DevWeight* w = find_w(c, name);
+  if (w->rows != rows || w->cols != cols)
+    return fail(c, TALOS_ERR_SHAPE, "resident \"%s\" is [%zu, %zu], call asks [%zu, %zu]", name, w->rows, w->cols,
+                rows, cols);
+  if (c->mv_x_cap < cols) {
+    if (c->mv_x) (void)hipFree(c->mv_x);
+    c->mv_x = nullptr;
+    HIPCHK(c, hipMalloc(&c->mv_x, cols * 4));
+    c->mv_x_cap = cols;
+  }
+  if (c->mv_out_cap < rows) {
+    if (c->mv_out) (void)hipFree(c->mv_out);
+    c->mv_out = nullptr;
+    HIPCHK(c, hipMalloc(&c->mv_out, rows * 4));
+    c->mv_out_cap = rows;
+  }
+  HIPCHK(c, hipMemcpyAsync(c->mv_x, x, cols * 4, hipMemcpyHostToDevice, c->stream));
+  if ((rc = enqueue_matvec(c, w, c->mv_x, c->mv_out))) return rc;
+  HIPCHK(c, hipMemcpyAsync(out, c->mv_out, rows * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return TALOS_OK;
+}
+
+int talos_hip_matvec_dev(talos_hip_ctx* c, const char* name, const float* d_x, float* d_out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!name || !d_x || !d_out) return fail(c, TALOS_ERR_ARG, "null argument");
+  const DevWeight* w = find_w(c, name);
+  if (!w) return fail(c, TALOS_ERR_MISSING_WEIGHT, "weight \"%s\" is not resident", name);
+  return enqueue_matvec(c, w, d_x, d_out);
+}
+
+int talos_hip_bench_kernel(talos_hip_ctx* c, const char* kind, uint32_t reps, float* avg_us, double* bytes) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!kind || !avg_us || !bytes || !reps) return fail(c, TALOS_ERR_ARG, "bad argument");
+  if ((rc = set_device(c))) return rc;
+  if ((rc = alloc_acts(c))) return rc;
+  const std::string k(kind);
+  const auto& cf = c->cfg;
+  std::vector<LayerW> lw(cf.n_layer);
+  for (uint32_t l = 0; l < cf.n_layer; ++l)
+    if ((rc = layer_weights(c, l, &lw[l]))) return rc;
+  const float* onorm = nullptr;
+  const DevWeight* wout = nullptr;
+  if (k == "output") {
+    if ((rc = need_norm(c, "output_norm.weight", cf.n_embd, &onorm))) return rc;
+    if ((rc = need_matrix(c, "output.weight", cf.vocab_size, cf.n_embd, &wout))) return rc;
+  }
+  const double act = 4.0 * cf.n_embd;
+  double b = 0;
+  if (k == "qkv") b = (double)(lw[0].q->len + lw[0].k->len + lw[0].v->len) + 2 * act + 4.0 * 2 * c->kv_dim;
+  else if (k == "oproj") b = (double)lw[0].o->len + 3 * act;
+  else if (k == "gateup") b = (double)(lw[0].g->len + lw[0].u->len) + 2 * act + 4.0 * cf.n_ff;
+  else if (k == "down") b = (double)lw[0].d->len + 4.0 * cf.n_ff + 2 * act;
+  else if (k == "output") b = (double)wout->len + 2 * act + 4.0 * cf.vocab_size;
+  else return fail(c, TALOS_ERR_ARG, "unknown kernel kind \"%s\" (qkv, oproj, gateup, down, output)", kind);
+  // The qkv kernel appends K/V at the device position: start from pos 0.
+  if ((rc = set_state(c, 0, 0))) return rc;
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  auto launch = [&](uint32_t r) {
+    const uint32_t l = r % cf.n_layer;
+    if (k == "qkv") enq_qkv(c, l, lw[l]);
+    else if (k == "oproj") enq_resid(c, lw[l].o, c->atty, cf.n_embd, c->q);
+    else if (k == "gateup") enq_gateup(c, lw[l]);
+    else if (k == "down") enq_resid(c, lw[l].d, c->h, cf.n_ff, c->q);
+    else enq_output(c, wout, onorm);
+  };
+  launch(0);  // warm
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (uint32_t r = 0; r < reps; ++r) launch(r + 1);
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float ms = 0;
+  HIPCHK(c, hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *avg_us = ms * 1000.f / (float)reps;
+  *bytes = b;
+  return TALOS_OK;
+}
+
+void* talos_hip_stream(talos_hip_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int talos_hip_sync(talos_hip_ctx* c) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return TALOS_OK;
+}
+
+}  // extern "C"
