@@ -144,6 +144,14 @@ int talos_hip_matvec_dev(talos_hip_ctx* ctx, const char* name, const float* d_x,
 int talos_hip_bench_kernel(talos_hip_ctx* ctx, const char* kind, uint32_t reps, float* avg_us,
                            double* bytes);
 
+/* Profiling aid for the persistent decode kernel: run one device-token step
+ * (as talos_hip_forward_token) and record, per workgroup, a wall-clock mark
+ * at each phase boundary (11 per layer, then the head).  Writes nblocks *
+ * slots marks (cap must allow them) and the tick length in ns.  No reference
+ * counterpart. */
+int talos_hip_phase_timeline(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint64_t* marks, size_t cap,
+                             uint32_t* nblocks, uint32_t* slots, double* tick_ns);
+
 /* The context's HIP stream (hipStream_t), for callers that time or order
  * work around talos_hip_matvec_dev. */
 void* talos_hip_stream(talos_hip_ctx* ctx);

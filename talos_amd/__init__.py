@@ -68,6 +68,8 @@ _SIGS = {
     "talos_hip_matvec": (C.c_int, [_P, C.c_char_p, _P, C.c_size_t, C.c_uint32, C.c_size_t, C.c_size_t, _F, _F]),
     "talos_hip_matvec_dev": (C.c_int, [_P, C.c_char_p, _P, _P]),
     "talos_hip_bench_kernel": (C.c_int, [_P, C.c_char_p, C.c_uint32, _F, C.POINTER(C.c_double)]),
+    "talos_hip_phase_timeline": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64), C.c_size_t,
+                                            _U32, _U32, C.POINTER(C.c_double)]),
     "talos_hip_stream": (_P, [_P]),
     "talos_hip_sync": (C.c_int, [_P]),
     # include/talos_host.h
@@ -396,6 +398,21 @@ class Model:
         if rc:
             raise TalosError(rc, lib().talos_hip_last_error(h).decode())
         return us.value, b.value
+
+    def phase_timeline(self, token: int, pos: int):
+        """Per-workgroup wall-clock marks (ns) of one persistent-kernel step:
+        an array [nblocks, slots]."""
+        h = self.backend_handle()
+        cap = 1 << 22
+        marks = np.zeros(cap, np.uint64)
+        nb, sl = C.c_uint32(), C.c_uint32()
+        tick = C.c_double()
+        rc = lib().talos_hip_phase_timeline(h, token, pos, marks.ctypes.data_as(C.POINTER(C.c_uint64)), cap,
+                                            C.byref(nb), C.byref(sl), C.byref(tick))
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
+        t = marks[: nb.value * sl.value].reshape(nb.value, sl.value).astype(np.float64) * tick.value
+        return t
 
     def backend_handle(self) -> int:
         h = lib().talos_model_backend(self._h)

@@ -1,0 +1,96 @@
+// coherent.h -- cross-workgroup data exchange inside one persistent kernel.
+//
+// The per-XCD L2 caches of MI355X are not coherent with each other while a
+// kernel runs.  Data one workgroup produces for another therefore moves with
+// agent-scope relaxed atomic loads/stores (global_load/store ... sc1), and a
+// producer waits for its stores to complete (s_waitcnt) before it signals.
+// Every wait is bounded: on timeout the kernel records an error and stops
+// waiting, so it always drains.
+#pragma once
+#include "device_common.h"
+
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh_u(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_u(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_coh_i(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh_i(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes as two 8-byte coherent accesses (p 16-byte aligned).
+__device__ __forceinline__ f4 ld_coh4(const float* p) {
+  const uint64_t a = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return f4{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+            __uint_as_float((uint32_t)(b >> 32))};
+}
+__device__ __forceinline__ void st_coh4(float* p, f4 v) {
+  const uint64_t a = (uint64_t)__float_as_uint(v.x) | ((uint64_t)__float_as_uint(v.y) << 32);
+  const uint64_t b = (uint64_t)__float_as_uint(v.z) | ((uint64_t)__float_as_uint(v.w) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p + 2), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until this thread's outstanding memory operations have completed.
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
+#define TALOS_SPIN_LIMIT (1u << 20)
+
+struct GridSync {
+  uint32_t* flags;  // [nblocks * 16]: one 64-byte line per block
+  uint32_t* go;     // release word written by block 0
+  uint32_t* err;    // set to 1 when a wait timed out
+  uint32_t nblocks;
+};
+
+// Grid barrier with epoch `ep` (monotonic, compared modulo 2^32).  Every
+// block publishes its arrival; block 0 gathers all arrivals and publishes
+// `go`; the others wait for `go`.  All threads' prior coherent stores are
+// complete before the arrival is visible.
+__device__ __forceinline__ void grid_barrier(const GridSync& g, uint32_t ep) {
+  wait_mem();
+  __syncthreads();
+  __shared__ uint32_t timed_out;
+  if (threadIdx.x == 0) {
+    timed_out = ld_coh_u(g.err);
+    st_coh_u(g.flags + blockIdx.x * 16, ep);
+  }
+  __syncthreads();
+  const bool skip = timed_out != 0;
+  if (blockIdx.x == 0) {
+    if (!skip) {
+      for (uint32_t w = threadIdx.x; w < g.nblocks; w += blockDim.x) {
+        uint32_t s = 0;
+        while ((int32_t)(ld_coh_u(g.flags + w * 16) - ep) < 0) {
+          if (++s > TALOS_SPIN_LIMIT) {
+            st_coh_u(g.err, 1u);
+            break;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) st_coh_u(g.go, ep);
+  } else if (threadIdx.x == 0 && !skip) {
+    uint32_t s = 0;
+    while ((int32_t)(ld_coh_u(g.go) - ep) < 0) {
+      if (++s > TALOS_SPIN_LIMIT) {
+        st_coh_u(g.err, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}

@@ -6,7 +6,7 @@
 // and is captured once into a hipGraph.  The position and token live in a
 // device `state` block, so the same graph replays for every step.
 #pragma once
-#include "matvec.h"
+#include "mvstream.h"
 
 // state[] slots
 enum { ST_POS = 0, ST_TOKEN = 1, ST_ARGMAX = 2, ST_STEP = 3 };
@@ -41,58 +41,6 @@ static inline size_t stage_lds_bytes(int n, int need) {
   return f * 4;
 }
 
-// Chunks per lane per K-step: enough to keep ~4 loads in flight without
-// issuing dead chunks on the short 4096-column rows.
-template <uint32_t FMT, int U>
-__device__ __forceinline__ void dot_rows_u(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                           bool two, const float* xs, const float* xsum, int lane,
-                                           float& ya, float& yb) {
-  float accA = 0.f, accB = 0.f;
-  const int nc = (int)A.nchunk;
-  for (int c0 = 0; c0 < nc; c0 += U * TALOS_WAVE) {
-    float pa[U], pb[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int c = c0 + i * TALOS_WAVE + lane;
-      const int cc = c < nc ? c : nc - 1;
-      pa[i] = 0.f;
-      pb[i] = 0.f;
-      if (FMT == TALOS_FMT_F32) chunk_f32(A, ra, B, rb, two, xs, cc, pa[i], pb[i]);
-      else if (FMT == TALOS_FMT_Q4_0) chunk_q4_0(A, ra, B, rb, two, xs, xsum, cc, pa[i], pb[i]);
-      else if (FMT == TALOS_FMT_Q8_0) chunk_q8_0(A, ra, B, rb, two, xs, xsum, cc, pa[i], pb[i]);
-      else chunk_q6_k(A, ra, B, rb, two, xs, xsum, cc, pa[i], pb[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const bool ok = c0 + i * TALOS_WAVE + lane < nc;
-      accA += ok ? pa[i] : 0.f;
-      accB += ok ? pb[i] : 0.f;
-    }
-  }
-  ya = wave_sum(accA);
-  yb = two ? wave_sum(accB) : 0.f;
-}
-
-template <uint32_t FMT>
-__device__ __forceinline__ void dot_rows_fmt(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                             bool two, const float* xs, const float* xsum, int lane,
-                                             float& ya, float& yb) {
-  const int steps = ((int)A.nchunk + TALOS_WAVE - 1) / TALOS_WAVE;
-  if (steps >= 4) dot_rows_u<FMT, 4>(A, ra, B, rb, two, xs, xsum, lane, ya, yb);
-  else if (steps >= 2) dot_rows_u<FMT, 2>(A, ra, B, rb, two, xs, xsum, lane, ya, yb);
-  else dot_rows_u<FMT, 1>(A, ra, B, rb, two, xs, xsum, lane, ya, yb);
-}
-
-__device__ __forceinline__ void dot2(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb, bool two,
-                                     const XStage& X, int lane, float& ya, float& yb) {
-  switch (A.fmt) {
-    case TALOS_FMT_F32: dot_rows_fmt<TALOS_FMT_F32>(A, ra, B, rb, two, X.xs[0], X.xsum, lane, ya, yb); break;
-    case TALOS_FMT_Q4_0: dot_rows_fmt<TALOS_FMT_Q4_0>(A, ra, B, rb, two, X.xs[0], X.xsum, lane, ya, yb); break;
-    case TALOS_FMT_Q8_0: dot_rows_fmt<TALOS_FMT_Q8_0>(A, ra, B, rb, two, X.xs[0], X.xsum, lane, ya, yb); break;
-    default: dot_rows_fmt<TALOS_FMT_Q6_K>(A, ra, B, rb, two, X.xs[1], X.xsum, lane, ya, yb); break;
-  }
-}
-
 __device__ __forceinline__ DevMat pick3(const DevMat& a, const DevMat& b, const DevMat& c, int s) {
   return s == 0 ? a : (s == 1 ? b : c);
 }
@@ -100,9 +48,10 @@ __device__ __forceinline__ DevMat pick3(const DevMat& a, const DevMat& b, const 
 // ---------------------------------------------------------------- k_qkv --
 // rmsnorm(x, attn_norm) -> q/k/v rows -> RoPE(q, k) -> q buffer and the K/V
 // cache row at `pos` (src/model/llama.rs:118-130, src/math/ops.rs:48-61).
+// q, k and v share one format; a unit is R consecutive rows of one of them.
 struct QKVParams {
   DevMat m[3];
-  uint32_t units[3];  // row pairs per matrix
+  uint32_t units[3];  // units per matrix (rows / R)
   const float* x;
   const float* norm_w;
   float eps;
@@ -117,19 +66,19 @@ struct QKVParams {
   int need;
 };
 
+template <uint32_t FMT, int R, int U>
 __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
   extern __shared__ float smem[];
   const XStage X = carve_x(smem, P.n, P.need);
-  stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t total = P.units[0] + P.units[1] + P.units[2];
+  const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
+  const int nunits = ubase >= total ? 0 : (int)min(P.upw, total - ubase);
   const int pos = P.state[ST_POS];
   const uint32_t half = P.hd / 2;
-  for (uint32_t k = 0; k < P.upw; ++k) {
-    const uint32_t u = (blockIdx.x * 4 + wave) * P.upw + k;
-    if (u >= total) break;
-    int s = 0;
-    uint32_t p = u;
+  auto seg = [&](uint32_t u, int& s, uint32_t& p) {
+    s = 0;
+    p = u;
     if (p >= P.units[0]) {
       p -= P.units[0];
       s = 1;
@@ -138,36 +87,52 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
         s = 2;
       }
     }
-    const DevMat M = pick3(P.m[0], P.m[1], P.m[2], s);
-    const uint32_t r0 = 2 * p;
-    float y0, y1;
-    dot2(M, r0, M, r0 + 1, true, X, lane, y0, y1);
-    if (lane == 0) {
+  };
+  auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+    int s;
+    uint32_t p;
+    seg(ubase + k, s, p);
+    A0 = pick3(P.m[0], P.m[1], P.m[2], s);
+    A1 = A0;
+    r0 = p * R;
+    rmax = A0.rows;
+  };
+  auto stage = [&] {
+    stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
+  };
+  auto epi = [&](int k, const float(&y)[R]) {
+    if (lane != 0) return;
+    int s;
+    uint32_t p;
+    seg(ubase + k, s, p);
+    const uint32_t r0 = p * R;
+#pragma unroll
+    for (int r = 0; r < R; r += 2) {
+      const uint32_t row = r0 + r;
+      const float y0 = y[r], y1 = y[r + 1];
       if (s < 2) {
-        const uint32_t i = (r0 % P.hd) / 2;
+        const uint32_t i = (row % P.hd) / 2;
         const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
         const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
         const float a = y0 * c - y1 * sn;
         const float b = y0 * sn + y1 * c;
-        if (s == 0) {
-          P.q_out[r0] = a;
-          P.q_out[r0 + 1] = b;
-        } else {
-          P.kc[(size_t)pos * P.kv_dim + r0] = a;
-          P.kc[(size_t)pos * P.kv_dim + r0 + 1] = b;
-        }
+        float* dst = s == 0 ? P.q_out + row : P.kc + (size_t)pos * P.kv_dim + row;
+        dst[0] = a;
+        dst[1] = b;
       } else {
-        P.vc[(size_t)pos * P.kv_dim + r0] = y0;
-        P.vc[(size_t)pos * P.kv_dim + r0 + 1] = y1;
+        P.vc[(size_t)pos * P.kv_dim + row] = y0;
+        P.vc[(size_t)pos * P.kv_dim + row + 1] = y1;
       }
     }
-  }
+  };
+  mv_stream<FMT, R, U, false>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
 }
 
-// -------------------------------------------------------------- k_resid --
-// resid[r] += <W row r, x> : the o-projection and down-projection with the
-// residual add fused (src/model/llama.rs:157-161, 172-176).  Also the plain
-// store used by the standalone matvec and the output projection (k_out).
+// --------------------------------------------------------------- k_rows --
+// out[r] (+)= <W row r, x>: the o-projection and down-projection with the
+// residual add fused (src/model/llama.rs:157-161, 172-176), the output
+// projection after the final rmsnorm (llama.rs:180-181, 87-89), and the
+// standalone matvec.  A unit is R consecutive rows.
 struct RowParams {
   DevMat m;
   const float* x;
@@ -176,39 +141,46 @@ struct RowParams {
   uint32_t n;
   float* out;
   int accumulate;  // 1: out[r] += y, 0: out[r] = y
-  uint32_t units;  // row pairs
+  uint32_t units;  // ceil(rows / R)
   uint32_t upw;
   int need;
 };
 
+template <uint32_t FMT, int R, int U>
 __global__ __launch_bounds__(256) void k_rows(RowParams P) {
   extern __shared__ float smem[];
   const XStage X = carve_x(smem, P.n, P.need);
-  stage_x(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
-          P.need & 2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (uint32_t k = 0; k < P.upw; ++k) {
-    const uint32_t u = (blockIdx.x * 4 + wave) * P.upw + k;
-    if (u >= P.units) break;
-    const uint32_t r0 = 2 * u;
-    const bool two = r0 + 1 < P.m.rows;
-    float y0, y1;
-    dot2(P.m, r0, P.m, two ? r0 + 1 : r0, two, X, lane, y0, y1);
-    if (lane == 0) {
-      if (P.accumulate) {
-        P.out[r0] += y0;
-        if (two) P.out[r0 + 1] += y1;
-      } else {
-        P.out[r0] = y0;
-        if (two) P.out[r0 + 1] = y1;
+  const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
+  const int nunits = ubase >= P.units ? 0 : (int)min(P.upw, P.units - ubase);
+  auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+    A0 = P.m;
+    A1 = P.m;
+    r0 = (ubase + k) * R;
+    rmax = P.m.rows;
+  };
+  auto stage = [&] {
+    stage_x(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
+            P.need & 2);
+  };
+  auto epi = [&](int k, const float(&y)[R]) {
+    const uint32_t r0 = (ubase + k) * R;
+    if (lane != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (r0 + r < P.m.rows) {
+        if (P.accumulate) P.out[r0 + r] += y[r];
+        else P.out[r0 + r] = y[r];
       }
     }
-  }
+  };
+  mv_stream<FMT, R, U, false>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
 }
 
 // ------------------------------------------------------------- k_gateup --
-// rmsnorm(x, ffn_norm) -> gate row p and up row p -> silu(g)*u
-// (src/model/llama.rs:164-171, src/math/ops.rs:28-37).
+// rmsnorm(x, ffn_norm) -> gate and up rows -> silu(g)*u (src/model/
+// llama.rs:164-171, src/math/ops.rs:28-37).  A unit is R/2 (gate, up) row
+// pairs, interleaved so one x read serves both matrices.
 struct GateUpParams {
   DevMat g, u;
   const float* x;
@@ -216,37 +188,52 @@ struct GateUpParams {
   float eps;
   uint32_t n;
   float* h;
-  uint32_t units;  // n_ff
+  uint32_t units;  // ceil(n_ff / (R/2))
   uint32_t upw;
   int need;
 };
 
+template <uint32_t FMT, int R, int U>
 __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
   extern __shared__ float smem[];
   const XStage X = carve_x(smem, P.n, P.need);
-  stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool same = P.g.fmt == P.u.fmt;
-  for (uint32_t k = 0; k < P.upw; ++k) {
-    const uint32_t p = (blockIdx.x * 4 + wave) * P.upw + k;
-    if (p >= P.units) break;
-    float yg, yu, dummy;
-    if (same) {
-      dot2(P.g, p, P.u, p, true, X, lane, yg, yu);
-    } else {
-      dot2(P.g, p, P.g, p, false, X, lane, yg, dummy);
-      dot2(P.u, p, P.u, p, false, X, lane, yu, dummy);
+  const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
+  const int nunits = ubase >= P.units ? 0 : (int)min(P.upw, P.units - ubase);
+  constexpr int PR = R / 2;
+  auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+    A0 = P.g;
+    A1 = P.u;
+    r0 = (ubase + k) * PR;
+    rmax = P.g.rows;
+  };
+  auto stage = [&] {
+    stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
+  };
+  auto epi = [&](int k, const float(&y)[R]) {
+    const uint32_t p0 = (ubase + k) * PR;
+    if (lane != 0) return;
+#pragma unroll
+    for (int r = 0; r < PR; ++r) {
+      if (p0 + r < P.g.rows) {
+        const float g = y[2 * r], u = y[2 * r + 1];
+        P.h[p0 + r] = (g / (1.0f + expf(-g))) * u;
+      }
     }
-    if (lane == 0) P.h[p] = (yg / (1.0f + expf(-yg))) * yu;
-  }
+  };
+  mv_stream<FMT, R, U, true>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
 }
 
 // ---------------------------------------------------------------- k_attn --
-// GQA decode attention for one KV head and one slice of positions
-// (src/model/llama.rs:135-155): scores = <q_h, K_t> * scale, softmax,
-// o = sum_t p_t V_t, with an online (max-shifted) softmax per slice.  Slices
-// are combined by the last block to finish for that KV head, in slice
-// order, so results do not depend on block timing.
+// GQA decode attention for one KV head and one slice of at most
+// TALOS_ATTN_CHUNK positions (src/model/llama.rs:135-155): scores =
+// <q_h, K_t> * scale, max-shifted softmax, o = sum_t p_t V_t.  The number of
+// slices follows the live sequence length (ceil(seq / chunk), at most
+// nsplit), so short sequences need no combine.  Slices are combined by the
+// last block to finish for that KV head, in slice order, so results do not
+// depend on block timing.
+#define TALOS_ATTN_CHUNK 64
+
 struct AttnParams {
   const float* q;
   const float* kc;
@@ -255,13 +242,16 @@ struct AttnParams {
   float* part;      // [n_kv][nsplit][group][hd + 2]
   uint32_t* count;  // [n_kv], self-resetting
   const int32_t* state;
-  uint32_t hd, kv_dim, group, nsplit, max_chunk;
+  uint32_t hd, kv_dim, group, nsplit;
+  uint32_t max_chunk;  // ceil(context_length / nsplit) >= any live slice
   float scale;
 };
 
-static inline size_t attn_lds_bytes(uint32_t hd, uint32_t group, uint32_t max_chunk) {
+static inline size_t attn_lds_bytes(uint32_t hd, uint32_t group, uint32_t nsplit, uint32_t max_chunk) {
   const uint32_t ns = 256 / hd;
-  return (size_t)(group * max_chunk + ns * group * hd + group * hd + 64) * 4;
+  const uint32_t comb = 3 * nsplit * group;
+  const uint32_t body = group * max_chunk + ns * group * hd;
+  return (size_t)((body > comb ? body : comb) + group * hd + 64) * 4;
 }
 
 template <int DPL>
@@ -269,17 +259,22 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
   extern __shared__ float smem[];
   const uint32_t hd = P.hd, group = P.group;
   const uint32_t ns = 256 / hd;
-  float* sc = smem;                          // [group][max_chunk]
-  float* ored = sc + group * P.max_chunk;    // [ns][group][hd]
-  float* qs = ored + ns * group * hd;        // [group][hd]
-  float* red = qs + group * hd;              // 64 floats
+  const uint32_t mc = P.max_chunk;
+  float* sc = smem;                             // [group][max_chunk]
+  float* ored = sc + group * mc;                // [ns][group][hd]
+  const uint32_t comb = 3 * P.nsplit * group;
+  const uint32_t body = group * mc + ns * group * hd;
+  float* qs = smem + (body > comb ? body : comb);  // [group][hd]
   __shared__ float mh[TALOS_MAX_GROUP], lh[TALOS_MAX_GROUP];
   __shared__ int am_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t j = blockIdx.x, split = blockIdx.y;
   const int seq = P.state[ST_POS] + 1;
-  const int chunk = (seq + (int)P.nsplit - 1) / (int)P.nsplit;
+  int nsp = (seq + TALOS_ATTN_CHUNK - 1) / TALOS_ATTN_CHUNK;
+  if (nsp > (int)P.nsplit) nsp = (int)P.nsplit;
+  if ((int)split >= nsp) return;  // uniform per block
+  const int chunk = (seq + nsp - 1) / nsp;
   const int t0 = (int)split * chunk;
   const int t1 = min(seq, t0 + chunk);
   const int len = max(0, t1 - t0);
@@ -287,81 +282,96 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
   for (uint32_t i = tid; i < group * hd; i += 256) qs[i] = P.q[(size_t)j * group * hd + i];
   __syncthreads();
 
-  // scores: 16 lanes per position, DPL dims per lane, reduced over the 16
-  const int dl = lane & 15;
+  // scores: 16 lanes per position, DPL dims per lane; the block covers 16
+  // positions per round and issues all rounds' K loads before reducing.
+  const int dl = lane & 15, slot = wave * 4 + (lane >> 4);
   float qr[TALOS_MAX_GROUP][DPL];
 #pragma unroll
   for (int h = 0; h < TALOS_MAX_GROUP; ++h)
 #pragma unroll
     for (int i = 0; i < DPL; ++i) qr[h][i] = h < (int)group ? qs[h * hd + dl * DPL + i] : 0.f;
-  for (int b = 0; b < len; b += 16) {
-    const int tl = b + wave * 4 + (lane >> 4);
-    const bool ok = tl < len;
-    const float* kp = P.kc + (size_t)(t0 + (ok ? tl : 0)) * P.kv_dim + j * hd + dl * DPL;
-    float kv[DPL];
-    if constexpr (DPL % 4 == 0) {
+  for (int b = 0; b < len; b += 64) {
+    float kv[4][DPL];
 #pragma unroll
-      for (int i = 0; i < DPL; i += 4) {
-        const f4 v = *reinterpret_cast<const f4*>(kp + i);
-        kv[i] = v.x;
-        kv[i + 1] = v.y;
-        kv[i + 2] = v.z;
-        kv[i + 3] = v.w;
+    for (int r = 0; r < 4; ++r) {
+      const int tl = b + r * 16 + slot;
+      const float* kp = P.kc + (size_t)(t0 + (tl < len ? tl : 0)) * P.kv_dim + j * hd + dl * DPL;
+      if constexpr (DPL % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < DPL; i += 4) {
+          const f4 v = *reinterpret_cast<const f4*>(kp + i);
+          kv[r][i] = v.x;
+          kv[r][i + 1] = v.y;
+          kv[r][i + 2] = v.z;
+          kv[r][i + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) kv[r][i] = kp[i];
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) kv[i] = kp[i];
     }
 #pragma unroll
-    for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
-      if (h < (int)group) {
-        float d = 0.f;
+    for (int r = 0; r < 4; ++r) {
+      const int tl = b + r * 16 + slot;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[h][i], kv[i], d);
-        d += __shfl_xor(d, 1, TALOS_WAVE);
-        d += __shfl_xor(d, 2, TALOS_WAVE);
-        d += __shfl_xor(d, 4, TALOS_WAVE);
-        d += __shfl_xor(d, 8, TALOS_WAVE);
-        if (ok && dl == 0) sc[h * P.max_chunk + tl] = d * P.scale;
+      for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
+        if (h < (int)group) {
+          float d = 0.f;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[h][i], kv[r][i], d);
+          d += __shfl_xor(d, 1, TALOS_WAVE);
+          d += __shfl_xor(d, 2, TALOS_WAVE);
+          d += __shfl_xor(d, 4, TALOS_WAVE);
+          d += __shfl_xor(d, 8, TALOS_WAVE);
+          if (tl < len && dl == 0) sc[h * mc + tl] = d * P.scale;
+        }
       }
     }
   }
   __syncthreads();
 
-  // softmax statistics per head over this slice; sc becomes exp(s - m)
-  for (uint32_t h = 0; h < group; ++h) {
+  // softmax statistics per head (one wave per head); sc becomes exp(s - m)
+  for (uint32_t h = wave; h < group; h += 4) {
     float m = -INFINITY;
-    for (int t = tid; t < len; t += 256) m = fmaxf(m, sc[h * P.max_chunk + t]);
+    for (int t = lane; t < len; t += 64) m = fmaxf(m, sc[h * mc + t]);
     m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
     float l = 0.f;
-    for (int t = tid; t < len; t += 256) {
-      const float e = expf(sc[h * P.max_chunk + t] - m);
-      sc[h * P.max_chunk + t] = e;
+    for (int t = lane; t < len; t += 64) {
+      const float e = expf(sc[h * mc + t] - m);
+      sc[h * mc + t] = e;
       l += e;
     }
-    l = block_sum(l, red, 4);
-    if (tid == 0) {
+    l = wave_sum(l);
+    if (lane == 0) {
       mh[h] = m;
       lh[h] = l;
     }
   }
   __syncthreads();
 
-  // o[h][d] = sum_t p[h][t] V_t[d]; ns position subsets per dim
+  // o[h][d] = sum_t p[h][t] V_t[d]; ns position subsets per dim, 4 loads in
+  // flight per thread
   const int d = tid % hd, sub = tid / hd;
   if (sub < (int)ns) {
     float acc[TALOS_MAX_GROUP];
 #pragma unroll
     for (int h = 0; h < TALOS_MAX_GROUP; ++h) acc[h] = 0.f;
-    for (int t = sub; t < len; t += ns) {
-      const float v = P.vc[(size_t)(t0 + t) * P.kv_dim + j * hd + d];
+    for (int t = sub; t < len; t += 4 * (int)ns) {
+      float v[4];
 #pragma unroll
-      for (int h = 0; h < TALOS_MAX_GROUP; ++h)
-        if (h < (int)group) acc[h] = __builtin_fmaf(sc[h * P.max_chunk + t], v, acc[h]);
+      for (int r = 0; r < 4; ++r) {
+        const int tt = t + r * (int)ns;
+        v[r] = tt < len ? P.vc[(size_t)(t0 + tt) * P.kv_dim + j * hd + d] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tt = t + r * (int)ns;
+        if (tt < len) {
+#pragma unroll
+          for (int h = 0; h < TALOS_MAX_GROUP; ++h)
+            if (h < (int)group) acc[h] = __builtin_fmaf(sc[h * mc + tt], v[r], acc[h]);
+        }
+      }
     }
 #pragma unroll
     for (int h = 0; h < TALOS_MAX_GROUP; ++h)
@@ -369,7 +379,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
   }
   __syncthreads();
 
-  if (P.nsplit == 1) {
+  if (nsp == 1) {
     for (uint32_t i = tid; i < group * hd; i += 256) {
       const uint32_t h = i / hd, dd = i % hd;
       float o = 0.f;
@@ -388,31 +398,54 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
     mypart[h * pstride + dd] = o;
   }
   if (tid < (int)group) {
-    mypart[tid * pstride + hd] = len > 0 ? mh[tid] : -INFINITY;
-    mypart[tid * pstride + hd + 1] = len > 0 ? lh[tid] : 0.f;
+    mypart[tid * pstride + hd] = mh[tid];
+    mypart[tid * pstride + hd + 1] = lh[tid];
   }
   __threadfence();
   __syncthreads();
   if (tid == 0) {
     const uint32_t old = atomicAdd(&P.count[j], 1u);
-    am_last = old == P.nsplit - 1;
+    am_last = old == (uint32_t)nsp - 1;
   }
   __syncthreads();
   if (!am_last) return;
   __threadfence();
+  // Combine: slice statistics into LDS (parallel loads), then weights.
   const float* parts = P.part + (size_t)j * P.nsplit * group * pstride;
+  float* cm = smem;                 // [nsp][group] m
+  float* cl = cm + nsp * group;     // [nsp][group] l
+  float* cw = cl + nsp * group;     // [nsp][group] exp(m - M)
+  for (int i = tid; i < nsp * (int)group; i += 256) {
+    const int s = i / (int)group, h = i % (int)group;
+    cm[i] = parts[((size_t)s * group + h) * pstride + hd];
+    cl[i] = parts[((size_t)s * group + h) * pstride + hd + 1];
+  }
+  __syncthreads();
+  if (tid < (int)group) {
+    float M = -INFINITY;
+    for (int s = 0; s < nsp; ++s) M = fmaxf(M, cm[s * group + tid]);
+    float L = 0.f;
+    for (int s = 0; s < nsp; ++s) {
+      const float w = expf(cm[s * group + tid] - M);
+      cw[s * group + tid] = w;
+      L = __builtin_fmaf(cl[s * group + tid], w, L);
+    }
+    lh[tid] = L;
+  }
+  __syncthreads();
   for (uint32_t i = tid; i < group * hd; i += 256) {
     const uint32_t h = i / hd, dd = i % hd;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < P.nsplit; ++s) M = fmaxf(M, parts[(s * group + h) * pstride + hd]);
-    float L = 0.f, O = 0.f;
-    for (uint32_t s = 0; s < P.nsplit; ++s) {
-      const float* ps = parts + (s * group + h) * pstride;
-      const float w = ps[hd + 1] > 0.f ? expf(ps[hd] - M) : 0.f;
-      L = __builtin_fmaf(ps[hd + 1], w, L);
-      O = __builtin_fmaf(ps[dd], w, O);
+    float O = 0.f;
+    int s = 0;
+    for (; s + 4 <= nsp; s += 4) {
+      float o4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o4[r] = parts[((size_t)(s + r) * group + h) * pstride + dd];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) O = __builtin_fmaf(o4[r], cw[(s + r) * group + h], O);
     }
-    P.out[((size_t)j * group + h) * hd + dd] = O / L;
+    for (; s < nsp; ++s) O = __builtin_fmaf(parts[((size_t)s * group + h) * pstride + dd], cw[s * group + h], O);
+    P.out[((size_t)j * group + h) * hd + dd] = O / lh[h];
   }
   if (tid == 0) atomicExch(&P.count[j], 0u);
 }

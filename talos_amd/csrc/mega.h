@@ -1,0 +1,663 @@
+// mega.h -- one persistent kernel per decode step.
+//
+// The whole token (src/model/llama.rs:96-183 plus the output projection and
+// the greedy argmax of src/sample.rs:7-14) runs in one cooperative launch of
+// one 512-thread workgroup per CU.  Phases per layer:
+//   qkv (rmsnorm + q/k/v + RoPE + K/V append) | attention | o + residual |
+//   rmsnorm + gate/up + SwiGLU | down + residual
+// then rmsnorm + output projection with a fused argmax.  A grid barrier
+// (coherent.h) separates dependent phases.  Each matvec phase issues its
+// first weight loads *before* waiting at the barrier that precedes it, so
+// HBM keeps streaming while the grid synchronizes.  Activations cross
+// workgroups only through coherent loads/stores.
+#pragma once
+#include "coherent.h"
+#include "kernels.h"
+
+#define MEGA_NT 512
+#define MEGA_NW (MEGA_NT / 64)
+
+// Slots of the device state block (int32), after ST_STEP.
+enum { ST_ERR = 8 };
+
+struct MegaLayer {
+  DevMat q, k, v, o, g, u, d;
+  const float* attn_norm;
+  const float* ffn_norm;
+  float* kc;
+  float* vc;
+};
+
+struct MegaParams {
+  const MegaLayer* layers;
+  uint32_t n_layer;
+  DevMat out_w;
+  const float* out_norm;
+  DevMat embd;
+  uint32_t n, ff, kv_dim, hd, group, n_kv, vocab;
+  float eps, scale;
+  const float* rope;
+  float* x;        // layer-0 input when the host supplies the embedding
+  float* xb[2];    // residual base per layer parity (xb[0] == x)
+  float* o_out;    // o-projection output of the current layer
+  float* d_out;    // down-projection output of the current layer
+  float* q;
+  float* atty;
+  float* h;
+  float* logits;
+  float* hidden;
+  float* part;
+  uint32_t* count;
+  int32_t* state;
+  int32_t* tokens;
+  uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
+  uint32_t nsplit, max_chunk;
+  int embed;   // 1: x = embedding row of the state token, looked up on the device
+  int hidden_only;
+  int argmax;  // 0: none, 1: argmax into state, 2: argmax + advance (greedy loop)
+  uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
+};
+
+// Phase timeline: per layer 11 marks (qkv staged/end, attention barrier/end,
+// o staged/end, gate-up staged/end, down staged/end, one spare), then head.
+#define MEGA_TL_PER_LAYER 11
+#define MEGA_TL_SLOTS(n_layer) ((n_layer) * MEGA_TL_PER_LAYER + 8)
+#define MEGA_MARK(P, slot)                                                                   \
+  do {                                                                                       \
+    if ((P).timeline && threadIdx.x == 0)                                                    \
+      (P).timeline[(size_t)blockIdx.x * MEGA_TL_SLOTS((P).n_layer) + (slot)] = wall_clock64(); \
+  } while (0)
+
+static inline size_t mega_sync_words(uint32_t nblocks) { return (size_t)nblocks * 16 + 64 + 2 * nblocks + 64; }
+
+// Stage n floats into the LDS layouts, optionally as rmsnorm(x)*w
+// (src/math/ops.rs:5-12), with every load of the block issued in one batch
+// (one memory round trip).  src(e) yields x[e..e+3] for e % 4 == 0; the
+// block also publishes the staged raw values of [pub_lo, pub_hi) to `pub`.
+// Requires n % 4 == 0 and n <= MEGA_STAGE_MAX.
+#define MEGA_VPT 8
+#define MEGA_STAGE_MAX (MEGA_VPT * MEGA_NT * 4)
+
+template <class Src>
+__device__ __forceinline__ void mega_stage(Src src, int n, const float* __restrict__ w, float eps, bool norm,
+                                           const XStage& X, int need, float* pub, int pub_lo, int pub_hi) {
+  // Opaque copy of the thread index: keeps the compiler from hoisting this
+  // index arithmetic out of the layer loop (which would keep it live, and
+  // spilled, across every phase).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int n4 = ((n + 15) & ~15) >> 2;
+  const int nr = n >> 2;  // real float4 groups
+  f4 v[MEGA_VPT];
+  // Loads are unconditional (index clamped) so they issue as one batch;
+  // out-of-range groups are zeroed afterwards.
+#pragma unroll
+  for (int i = 0; i < MEGA_VPT; ++i) {
+    const int e4 = i * MEGA_NT + tid;
+    v[i] = src((e4 < nr ? e4 : nr - 1) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < MEGA_VPT; ++i)
+    if (i * MEGA_NT + tid >= nr) v[i] = f4{0.f, 0.f, 0.f, 0.f};
+  float scale = 1.f;
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < MEGA_VPT; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = block_sum(ss, X.red, MEGA_NW);
+    scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < MEGA_VPT; ++i) {
+    const int e4 = i * MEGA_NT + tid;
+    f4 x = v[i];
+    if (e4 < n4) {
+      if (pub && e4 < nr && e4 * 4 >= pub_lo && e4 * 4 < pub_hi) st_coh4(pub + e4 * 4, x);
+      if (norm && e4 < nr) {
+        const f4 ww = *reinterpret_cast<const f4*>(w + e4 * 4);
+        x.x = x.x * scale * ww.x;
+        x.y = x.y * scale * ww.y;
+        x.z = x.z * scale * ww.z;
+        x.w = x.w * scale * ww.w;
+      }
+      if (need & 1) *reinterpret_cast<f4*>(X.xs[0] + xidx<0>(e4 * 4)) = x;
+      if (need & 2) *reinterpret_cast<f4*>(X.xs[1] + xidx<1>(e4 * 4)) = x;
+    }
+    float s = (x.x + x.y) + (x.z + x.w);
+    s += __shfl_xor(s, 1, TALOS_WAVE);
+    s += __shfl_xor(s, 2, TALOS_WAVE);
+    if (e4 < n4 && (tid & 3) == 0) X.xsum[e4 >> 2] = s;
+  }
+  __syncthreads();
+}
+
+// x[e..e+3] of one coherent array, of a + b, or of (a + b) + c: the residual
+// stream is kept as the layer's base plus the o-projection and down-
+// projection outputs, summed in the order of src/model/llama.rs:159-161,
+// 174-176.
+struct CohSrc {
+  const float* a;
+  __device__ __forceinline__ f4 operator()(int e) const { return ld_coh4(a + e); }
+};
+struct CohSrc2 {
+  const float *a, *b;
+  __device__ __forceinline__ f4 operator()(int e) const {
+    const f4 x = ld_coh4(a + e), y = ld_coh4(b + e);
+    return f4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+  }
+};
+struct CohSrc3 {
+  const float *a, *b, *c;
+  __device__ __forceinline__ f4 operator()(int e) const {
+    const f4 x = ld_coh4(a + e), y = ld_coh4(b + e), z = ld_coh4(c + e);
+    return f4{(x.x + y.x) + z.x, (x.y + y.y) + z.y, (x.z + y.z) + z.z, (x.w + y.w) + z.w};
+  }
+};
+
+struct EmbSrc {
+  DevMat M;
+  uint32_t tok;
+  __device__ __forceinline__ f4 operator()(int e) const {
+    return f4{dq_elem(M, tok, e), dq_elem(M, tok, e + 1), dq_elem(M, tok, e + 2), dq_elem(M, tok, e + 3)};
+  }
+};
+
+// Strided unit count for global wave gw of tw.
+__device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t tw) {
+  return gw < total ? (int)((total - gw + tw - 1) / tw) : 0;
+}
+
+// One attention work item: KV head j, positions [t0, t1) of at most
+// MEGA_ATTN_CHUNK (src/model/llama.rs:139-155 for the GQA group of j).  All
+// K, V and q loads are issued together (one memory round trip); K uses 16
+// lanes per position (DPL dims each), V uses 4*DPL lanes per position (a
+// float4 each).  Data this step wrote (q, the K/V row at `pos`, slice
+// partials) is read coherently.  With nsp > 1 slices the last block to
+// finish for head j merges them in slice order.
+#define MEGA_ATTN_CHUNK 128
+
+static inline __host__ __device__ uint32_t mega_attn_ppr(uint32_t hd) { return MEGA_NT / (hd / 4); }
+static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group, uint32_t nsplit) {
+  const size_t ored = (size_t)mega_attn_ppr(hd) * group * hd, comb = 3 * (size_t)nsplit * group;
+  return (size_t)group * hd + (size_t)group * MEGA_ATTN_CHUNK + (ored > comb ? ored : comb) + 64;
+}
+
+template <int DPL>
+__device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLayer& L, uint32_t j, int split,
+                                               int nsp, int pos, float* smem) {
+  constexpr int HD = 16 * DPL;            // head_dim
+  constexpr int TPP = HD / 4;             // V threads per position
+  constexpr int PPR = MEGA_NT / TPP;      // V positions per round
+  constexpr int VR = (MEGA_ATTN_CHUNK + PPR - 1) / PPR;
+  constexpr int KR = MEGA_ATTN_CHUNK / 32;  // K rounds of 32 positions
+  const uint32_t group = P.group;
+  float* qs = smem;                                  // [group][HD]
+  float* sc = qs + group * HD;                       // [group][CHUNK]
+  float* ored = sc + group * MEGA_ATTN_CHUNK;        // [PPR][group][HD]
+  __shared__ float mh[TALOS_MAX_GROUP], lh[TALOS_MAX_GROUP];
+  __shared__ int am_last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int seq = pos + 1;
+  const int chunk = (seq + nsp - 1) / nsp;
+  const int t0 = split * chunk;
+  const int t1 = min(seq, t0 + chunk);
+  const int len = max(0, t1 - t0);
+  const size_t hoff = (size_t)j * HD;
+
+  // K: lane group (16 lanes) per position
+  const int dl = lane & 15, slot = wave * 4 + (lane >> 4);
+  float kv[KR][DPL];
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    const int tl = r * 32 + slot;
+    const int t = t0 + (tl < len ? tl : 0);
+    const float* kp = L.kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
+    if (t == pos) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) kv[r][i] = ld_coh(kp + i);
+    } else if constexpr (DPL % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < DPL; i += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(kp + i);
+        kv[r][i] = v.x;
+        kv[r][i + 1] = v.y;
+        kv[r][i + 2] = v.z;
+        kv[r][i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) kv[r][i] = kp[i];
+    }
+  }
+  // V: TPP threads per position, a float4 each
+  const int vp = tid / TPP, vd = tid % TPP;
+  f4 vv[VR];
+#pragma unroll
+  for (int r = 0; r < VR; ++r) {
+    const int tl = r * PPR + vp;
+    if (vp < PPR && tl < len) {
+      const float* p = L.vc + (size_t)(t0 + tl) * P.kv_dim + hoff + vd * 4;
+      vv[r] = t0 + tl == pos ? ld_coh4(p) : *reinterpret_cast<const f4*>(p);
+    } else {
+      vv[r] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // q for the group's heads
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = ld_coh(P.q + (size_t)j * group * HD + i);
+  __syncthreads();
+
+  // scores
+#pragma unroll
+  for (int r = 0; r < KR; ++r) {
+    const int tl = r * 32 + slot;
+#pragma unroll
+    for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
+      if (h < (int)group) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qs[h * HD + dl * DPL + i], kv[r][i], d);
+        d += __shfl_xor(d, 1, TALOS_WAVE);
+        d += __shfl_xor(d, 2, TALOS_WAVE);
+        d += __shfl_xor(d, 4, TALOS_WAVE);
+        d += __shfl_xor(d, 8, TALOS_WAVE);
+        if (tl < len && dl == 0) sc[h * MEGA_ATTN_CHUNK + tl] = d * P.scale;
+      }
+    }
+  }
+  __syncthreads();
+  // softmax statistics (one wave per head); sc becomes exp(s - m)
+  for (uint32_t h = wave; h < group; h += MEGA_NW) {
+    float mx = -INFINITY;
+    for (int t = lane; t < len; t += 64) mx = fmaxf(mx, sc[h * MEGA_ATTN_CHUNK + t]);
+    mx = wave_max(mx);
+    float l = 0.f;
+    for (int t = lane; t < len; t += 64) {
+      const float e = expf(sc[h * MEGA_ATTN_CHUNK + t] - mx);
+      sc[h * MEGA_ATTN_CHUNK + t] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      mh[h] = mx;
+      lh[h] = l;
+    }
+  }
+  __syncthreads();
+  // o[h][4vd..4vd+3] partial over this thread's positions
+  if (vp < PPR) {
+    f4 acc[TALOS_MAX_GROUP];
+#pragma unroll
+    for (int h = 0; h < TALOS_MAX_GROUP; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+      const int tl = r * PPR + vp;
+      if (tl < len) {
+#pragma unroll
+        for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
+          if (h < (int)group) {
+            const float p = sc[h * MEGA_ATTN_CHUNK + tl];
+            acc[h].x = __builtin_fmaf(p, vv[r].x, acc[h].x);
+            acc[h].y = __builtin_fmaf(p, vv[r].y, acc[h].y);
+            acc[h].z = __builtin_fmaf(p, vv[r].z, acc[h].z);
+            acc[h].w = __builtin_fmaf(p, vv[r].w, acc[h].w);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < TALOS_MAX_GROUP; ++h)
+      if (h < (int)group) *reinterpret_cast<f4*>(ored + ((size_t)vp * group + h) * HD + vd * 4) = acc[h];
+  }
+  __syncthreads();
+
+  if (nsp == 1) {
+    for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
+      const uint32_t h = i / HD, dd = i % HD;
+      float o = 0.f;
+      for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
+      st_coh(P.atty + ((size_t)j * group + h) * HD + dd, o / lh[h]);
+    }
+    __syncthreads();
+    return;
+  }
+
+  const size_t pstride = HD + 2;
+  float* mypart = P.part + ((size_t)j * P.nsplit + split) * group * pstride;
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
+    const uint32_t h = i / HD, dd = i % HD;
+    float o = 0.f;
+    for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
+    st_coh(mypart + h * pstride + dd, o);
+  }
+  if (tid < (int)group) {
+    st_coh(mypart + tid * pstride + HD, mh[tid]);
+    st_coh(mypart + tid * pstride + HD + 1, lh[tid]);
+  }
+  wait_mem();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(P.count + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    am_last = old == (uint32_t)nsp - 1;
+  }
+  __syncthreads();
+  if (am_last) {
+    const float* parts = P.part + (size_t)j * P.nsplit * group * pstride;
+    float* cm = sc;  // reuses the score / reduction scratch
+    float* cl = cm + nsp * group;
+    float* cw = cl + nsp * group;
+    for (int i = tid; i < nsp * (int)group; i += MEGA_NT) {
+      const int s = i / (int)group, h = i % (int)group;
+      cm[i] = ld_coh(parts + ((size_t)s * group + h) * pstride + HD);
+      cl[i] = ld_coh(parts + ((size_t)s * group + h) * pstride + HD + 1);
+    }
+    __syncthreads();
+    if (tid < (int)group) {
+      float M = -INFINITY;
+      for (int s = 0; s < nsp; ++s) M = fmaxf(M, cm[s * group + tid]);
+      float Ls = 0.f;
+      for (int s = 0; s < nsp; ++s) {
+        const float w = expf(cm[s * group + tid] - M);
+        cw[s * group + tid] = w;
+        Ls = __builtin_fmaf(cl[s * group + tid], w, Ls);
+      }
+      lh[tid] = Ls;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
+      const uint32_t h = i / HD, dd = i % HD;
+      float O = 0.f;
+      int s = 0;
+      for (; s + 4 <= nsp; s += 4) {
+        float o4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o4[r] = ld_coh(parts + ((size_t)(s + r) * group + h) * pstride + dd);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) O = __builtin_fmaf(o4[r], cw[(s + r) * group + h], O);
+      }
+      for (; s < nsp; ++s) O = __builtin_fmaf(ld_coh(parts + ((size_t)s * group + h) * pstride + dd), cw[s * group + h], O);
+      st_coh(P.atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
+    }
+    if (tid == 0) st_coh_u(P.count + j, 0u);
+  }
+  __syncthreads();
+}
+
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL>
+__global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t nb = gridDim.x;
+  const uint32_t gw = blockIdx.x * MEGA_NW + wave, tw = nb * MEGA_NW;
+  GridSync G;
+  G.flags = P.sync;
+  G.go = P.sync + nb * 16;
+  G.err = reinterpret_cast<uint32_t*>(P.state + ST_ERR);
+  G.nblocks = nb;
+  uint32_t* epoch_p = P.sync + nb * 16 + 16;
+  uint32_t* done = P.sync + nb * 16 + 32;
+  int32_t* amx = reinterpret_cast<int32_t*>(P.sync + nb * 16 + 64);
+  uint32_t ep = ld_coh_u(epoch_p);
+  const int pos = P.state[ST_POS];
+  const uint32_t tok = (uint32_t)P.state[ST_TOKEN];
+  const uint32_t half = P.hd / 2;
+  constexpr int RL = mv_rows(LF), RO = mv_rows(OF);
+  constexpr int LL = MvT<LF>::L, LO = MvT<OF>::L;
+  const int need_l = 1 << LL, need_o = 1 << LO;
+  // this block's slice of the residual base it publishes each layer
+  const int slice = (((int)P.n + (int)nb - 1) / (int)nb + 3) & ~3;
+  const int pub_lo = (int)blockIdx.x * slice, pub_hi = pub_lo + slice;
+
+  for (uint32_t l = 0; l < P.n_layer; ++l) {
+    const MegaLayer& L = P.layers[l];
+    float* base = P.xb[l & 1];
+    // ---- qkv: rmsnorm(x) -> q/k/v -> RoPE -> q, K/V row at pos
+    {
+      const XStage X = carve_x(smem, P.n, need_l);
+      const uint32_t u0 = P.n / RL, u1 = P.kv_dim / RL, total = u0 + 2 * u1;
+      auto seg = [&](uint32_t u, int& s, uint32_t& p) {
+        s = u < u0 ? 0 : (u < u0 + u1 ? 1 : 2);
+        p = s == 0 ? u : (s == 1 ? u - u0 : u - u0 - u1);
+      };
+      auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+        int s;
+        uint32_t p;
+        seg(gw + (uint32_t)k * tw, s, p);
+        A0 = pick3(L.q, L.k, L.v, s);
+        A1 = A0;
+        r0 = p * RL;
+        rmax = A0.rows;
+      };
+      auto stage = [&] {
+        if (l > 0) {
+          grid_barrier(G, ++ep);
+          // x = (base + attproj) + down of the previous layer; publish it
+          CohSrc3 src{P.xb[(l - 1) & 1], P.o_out, P.d_out};
+          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+        } else if (P.embed) {
+          EmbSrc src{P.embd, tok};
+          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+        } else {
+          CohSrc src{P.x};
+          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+        }
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
+      };
+      auto epi = [&](int k, const float(&y)[RL]) {
+        if (lane != 0) return;
+        int s;
+        uint32_t p;
+        seg(gw + (uint32_t)k * tw, s, p);
+        const uint32_t r0 = p * RL;
+#pragma unroll
+        for (int r = 0; r < RL; r += 2) {
+          const uint32_t row = r0 + r;
+          const float y0 = y[r], y1 = y[r + 1];
+          if (s < 2) {
+            const uint32_t i = (row % P.hd) / 2;
+            const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
+            const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
+            float* dst = s == 0 ? P.q + row : L.kc + (size_t)pos * P.kv_dim + row;
+            st_coh(dst, y0 * c - y1 * sn);
+            st_coh(dst + 1, y0 * sn + y1 * c);
+          } else {
+            st_coh(L.vc + (size_t)pos * P.kv_dim + row, y0);
+            st_coh(L.vc + (size_t)pos * P.kv_dim + row + 1, y1);
+          }
+        }
+      };
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
+    }
+    // ---- attention over positions 0..pos
+    {
+      grid_barrier(G, ++ep);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 2);
+      const int seq = pos + 1;
+      int nsp = (seq + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK;
+      if (nsp > (int)P.nsplit) nsp = (int)P.nsplit;
+      const uint32_t items = P.n_kv * (uint32_t)nsp;
+      for (uint32_t it = blockIdx.x; it < items; it += nb)
+        mega_attn_item<DPL>(P, L, it % P.n_kv, (int)(it / P.n_kv), nsp, pos, smem);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);
+    }
+    // ---- o-projection (the residual add happens where x is next read)
+    {
+      const XStage X = carve_x(smem, P.n, need_l);
+      const uint32_t total = P.n / RL;
+      auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+        A0 = L.o;
+        A1 = L.o;
+        r0 = (gw + (uint32_t)k * tw) * RL;
+        rmax = L.o.rows;
+      };
+      auto stage = [&] {
+        grid_barrier(G, ++ep);
+        CohSrc src{P.atty};
+        mega_stage(src, P.n, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
+      };
+      auto epi = [&](int k, const float(&y)[RL]) {
+        if (lane != 0) return;
+        const uint32_t r0 = (gw + (uint32_t)k * tw) * RL;
+#pragma unroll
+        for (int r = 0; r < RL; ++r) st_coh(P.o_out + r0 + r, y[r]);
+      };
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
+    }
+    // ---- rmsnorm(base + attproj) + gate/up + SwiGLU
+    {
+      const XStage X = carve_x(smem, P.n, need_l);
+      constexpr int PR = RL / 2;
+      const uint32_t total = (P.ff + PR - 1) / PR;
+      auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+        A0 = L.g;
+        A1 = L.u;
+        r0 = (gw + (uint32_t)k * tw) * PR;
+        rmax = L.g.rows;
+      };
+      auto stage = [&] {
+        grid_barrier(G, ++ep);
+        CohSrc2 src{base, P.o_out};
+        mega_stage(src, P.n, L.ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
+      };
+      auto epi = [&](int k, const float(&y)[RL]) {
+        if (lane != 0) return;
+        const uint32_t p0 = (gw + (uint32_t)k * tw) * PR;
+#pragma unroll
+        for (int r = 0; r < PR; ++r) {
+          if (p0 + r < P.ff) {
+            const float g = y[2 * r], u = y[2 * r + 1];
+            st_coh(P.h + p0 + r, (g / (1.0f + expf(-g))) * u);
+          }
+        }
+      };
+      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
+    }
+    // ---- down-projection (2-row units keep the long rows' double buffer in
+    // registers)
+    {
+      constexpr int RD = 2;
+      const XStage X = carve_x(smem, P.ff, need_l);
+      const uint32_t total = P.n / RD;
+      auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+        A0 = L.d;
+        A1 = L.d;
+        r0 = (gw + (uint32_t)k * tw) * RD;
+        rmax = L.d.rows;
+      };
+      auto stage = [&] {
+        grid_barrier(G, ++ep);
+        CohSrc src{P.h};
+        mega_stage(src, P.ff, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
+      };
+      auto epi = [&](int k, const float(&y)[RD]) {
+        if (lane != 0) return;
+        const uint32_t r0 = (gw + (uint32_t)k * tw) * RD;
+#pragma unroll
+        for (int r = 0; r < RD; ++r) st_coh(P.d_out + r0 + r, y[r]);
+      };
+      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
+    }
+  }
+
+  // ---- head: final rmsnorm of (base + attproj) + down, then logits (+
+  // argmax) or the hidden state
+  const float* last = P.xb[(P.n_layer - 1) & 1];
+  __shared__ int32_t wk[MEGA_NW], wi[MEGA_NW];
+  int32_t bk = INT32_MIN, bi = -1;
+  if (P.hidden_only) {
+    grid_barrier(G, ++ep);
+    if (blockIdx.x == 0) {
+      float ss = 0.f;
+      for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
+        const float v = (ld_coh(last + i) + ld_coh(P.o_out + i)) + ld_coh(P.d_out + i);
+        ss += v * v;
+      }
+      ss = block_sum(ss, smem, MEGA_NW);
+      const float scale = 1.0f / sqrtf(ss / (float)P.n + P.eps);
+      for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
+        const float v = (ld_coh(last + i) + ld_coh(P.o_out + i)) + ld_coh(P.d_out + i);
+        P.hidden[i] = v * scale * P.out_norm[i];
+      }
+    }
+  } else {
+    const XStage X = carve_x(smem, P.n, need_o);
+    const uint32_t total = (P.vocab + RO - 1) / RO;
+    auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+      A0 = P.out_w;
+      A1 = P.out_w;
+      r0 = (gw + (uint32_t)k * tw) * RO;
+      rmax = P.out_w.rows;
+    };
+    auto stage = [&] {
+      grid_barrier(G, ++ep);
+      CohSrc3 src{last, P.o_out, P.d_out};
+      mega_stage(src, P.n, P.out_norm, P.eps, true, X, need_o, nullptr, 0, 0);
+      MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
+    };
+    auto epi = [&](int k, const float(&y)[RO]) {
+      if (lane != 0) return;
+      const uint32_t r0 = (gw + (uint32_t)k * tw) * RO;
+#pragma unroll
+      for (int r = 0; r < RO; ++r) {
+        if (r0 + r < P.vocab) {
+          P.logits[r0 + r] = y[r];
+          const int32_t key = total_key(y[r]);
+          if (key > bk || (key == bk && (int32_t)(r0 + r) > bi)) {
+            bk = key;
+            bi = (int32_t)(r0 + r);
+          }
+        }
+      }
+    };
+    mv_stream<OF, RO, UO, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LO], X.xsum, lane);
+    MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 1);
+  }
+  // per-block best, then the last block to finish reduces and advances state
+  if (lane == 0) {
+    wk[wave] = bk;
+    wi[wave] = bi;
+  }
+  __syncthreads();
+  __shared__ int am_last;
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < MEGA_NW; ++w)
+      if (wk[w] > bk || (wk[w] == bk && wi[w] > bi)) {
+        bk = wk[w];
+        bi = wi[w];
+      }
+    st_coh_i(amx + 2 * blockIdx.x, bk);
+    st_coh_i(amx + 2 * blockIdx.x + 1, bi);
+    wait_mem();
+    const uint32_t old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    am_last = old == nb - 1;
+  }
+  __syncthreads();
+  if (am_last && threadIdx.x == 0) {
+    int32_t k = INT32_MIN, i = -1;
+    for (uint32_t b = 0; b < nb; ++b) {
+      const int32_t kb = ld_coh_i(amx + 2 * b), ib = ld_coh_i(amx + 2 * b + 1);
+      if (kb > k || (kb == k && ib > i)) {
+        k = kb;
+        i = ib;
+      }
+    }
+    if (P.argmax) {
+      P.state[ST_ARGMAX] = i;
+      if (P.argmax == 2) {
+        const int32_t step = P.state[ST_STEP];
+        P.tokens[step] = i;
+        P.state[ST_TOKEN] = i;
+        P.state[ST_POS] = pos + 1;
+        P.state[ST_STEP] = step + 1;
+      }
+    }
+    st_coh_u(epoch_p, ep);
+    st_coh_u(done, 0u);
+  }
+}

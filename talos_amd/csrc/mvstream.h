@@ -1,0 +1,187 @@
+// mvstream.h -- double-buffered weight streaming for the decode matvecs.
+//
+// A wave owns a run of "units" (R output rows of one matrix, or R/2 row pairs
+// of two matrices for gate/up) and walks each unit's columns in "items" of
+// U chunks per lane.  While it computes item i, the loads of item i+1 are in
+// flight; the first item's loads are issued before the block stages x into
+// LDS, so the HBM latency of the weights overlaps the rmsnorm/x setup.
+// Weights are read once with 128-bit non-temporal loads; x comes from LDS and
+// is shared by the R rows of an item.
+#pragma once
+#include "matvec.h"
+
+// Rows per unit for each format (register budget: Q8_0 and Q6_K carry 2-3
+// 128-bit words per chunk, so they take two rows).
+static inline __host__ __device__ constexpr int mv_rows(uint32_t fmt) {
+  return (fmt == TALOS_FMT_Q8_0 || fmt == TALOS_FMT_Q6_K) ? 2 : 4;
+}
+// Chunk-steps per item: up to 4, fewer for short rows.
+static inline __host__ __device__ int mv_u(uint32_t nchunk) {
+  const uint32_t steps = (nchunk + 63) / 64;
+  return steps >= 4 ? 4 : (steps >= 2 ? 2 : 1);
+}
+
+template <uint32_t FMT>
+struct MvT {
+  static constexpr int QW = FMT == TALOS_FMT_Q8_0 ? 2 : FMT == TALOS_FMT_Q6_K ? 3 : 1;  // u4 per chunk
+  static constexpr int L = FMT == TALOS_FMT_Q6_K ? 1 : 0;                                // x layout
+};
+
+template <uint32_t FMT, int R, int U>
+struct MvBuf {
+  u4 q[R][U][MvT<FMT>::QW];
+  uint32_t a[R][U];  // Q4_0/Q8_0: f16 scale bits; Q6_K: packed sub-scales
+  uint32_t b[R][U];  // Q6_K: f16 super-scale bits
+};
+
+// Load one item: rows r0 + slot (clamped to rmax - 1; the caller masks
+// those results), chunks c0 + u*64 + lane (clamped to nchunk - 1, masked in
+// mv_compute).  PAIR interleaves two matrices: slot 2k -> A0 row r0+k,
+// slot 2k+1 -> A1 row r0+k.
+template <uint32_t FMT, int R, int U, bool PAIR>
+__device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, const DevMat& A1, uint32_t r0,
+                                        uint32_t rmax, int c0, int lane) {
+  const int nc = (int)A0.nchunk;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const DevMat& M = (PAIR && (i & 1)) ? A1 : A0;
+    uint32_t row = PAIR ? r0 + i / 2 : r0 + i;
+    row = row < rmax ? row : rmax - 1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int c = c0 + u * TALOS_WAVE + lane;
+      c = c < nc ? c : nc - 1;
+      const size_t ci = (size_t)row * nc + c;
+      if (FMT == TALOS_FMT_F32) {
+        B.q[i][u][0] = ldg4(M.q + ci * 16);
+      } else if (FMT == TALOS_FMT_Q4_0) {
+        B.q[i][u][0] = ldg4(M.q + ci * 16);
+        B.a[i][u] = M.d[ci];
+      } else if (FMT == TALOS_FMT_Q8_0) {
+        B.q[i][u][0] = ldg4(M.q + ci * 32);
+        B.q[i][u][MvT<FMT>::QW - 1] = ldg4(M.q + ci * 32 + 16);
+        B.a[i][u] = M.d[ci];
+      } else {
+        const uint8_t* p = M.q + (size_t)row * nc * 48 + (size_t)c * 16;
+        B.q[i][u][0] = ldg4(p);
+        B.q[i][u][MvT<FMT>::QW > 1 ? 1 : 0] = ldg4(p + (size_t)nc * 16);
+        B.q[i][u][MvT<FMT>::QW - 1] = ldg4(p + (size_t)nc * 32);
+        B.a[i][u] = M.sc[ci];
+        B.b[i][u] = M.d[(size_t)row * (nc >> 2) + (c >> 2)];
+      }
+    }
+  }
+}
+
+// acc[i] += <row slot i, x> over this item's chunks.
+template <uint32_t FMT, int R, int U>
+__device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const float* xs, const float* xsum, int nc,
+                                           int c0, int lane, float (&acc)[R]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * TALOS_WAVE + lane;
+    const bool ok = c < nc;
+    const int cc = ok ? c : nc - 1;
+    if (FMT == TALOS_FMT_F32) {
+      f4 x = lds4(xs, xidx<0>(cc * 4));
+      if (!ok) x = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const f4 w = __builtin_bit_cast(f4, B.q[i][u][0]);
+        float a = acc[i];
+        a = __builtin_fmaf(w.x, x.x, a);
+        a = __builtin_fmaf(w.y, x.y, a);
+        a = __builtin_fmaf(w.z, x.z, a);
+        a = __builtin_fmaf(w.w, x.w, a);
+        acc[i] = a;
+      }
+    } else if (FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0) {
+      f4 x[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = lds4(xs, xidx<0>(cc * 32 + k * 4));
+      const float xsb = xsum[2 * cc] + xsum[2 * cc + 1];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const float d = ok ? f16_to_f32((uint16_t)B.a[i][u]) : 0.f;
+        const float p = FMT == TALOS_FMT_Q4_0
+                            ? q4_block_dot(B.q[i][u][0], x, 8.f * xsb)
+                            : q8_block_dot(B.q[i][u][0], B.q[i][u][MvT<FMT>::QW - 1], x, 128.f * xsb);
+        acc[i] = __builtin_fmaf(d, p, acc[i]);
+      }
+    } else {
+      const int base = (cc >> 2) * 256 + ((cc >> 1) & 1) * 128 + (cc & 1) * 16;
+      f4 x[16];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[r * 4 + k] = lds4(xs, xidx<1>(base + r * 32 + k * 4));
+      float xsr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xsr[r] = 32.f * xsum[(base + r * 32) >> 4];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const float d = ok ? f16_to_f32((uint16_t)B.b[i][u]) : 0.f;
+        const float p = q6_chunk_dot(B.q[i][u][0], B.q[i][u][MvT<FMT>::QW > 1 ? 1 : 0],
+                                     B.q[i][u][MvT<FMT>::QW - 1], B.a[i][u], x, xsr);
+        acc[i] = __builtin_fmaf(d, p, acc[i]);
+      }
+    }
+  }
+}
+
+// Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
+// unit of the wave (returns false past the end); epi(k, y) consumes the R
+// row results (every lane holds them).  `stage` is called once by every
+// thread of the block, after the first item's loads are issued.
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class StageFn, class EpiFn>
+__device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, StageFn stage, EpiFn epi, const float* xs,
+                                          const float* xsum, int lane) {
+  MvBuf<FMT, R, U> b0, b1;
+  int nc = 1, iters = 1;
+  DevMat A0{}, A1{};
+  uint32_t r0 = 0, rmax = 1;
+  if (nunits > 0) {
+    unit(0, A0, A1, r0, rmax);
+    nc = (int)A0.nchunk;
+    iters = (nc + U * TALOS_WAVE - 1) / (U * TALOS_WAVE);
+    mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
+  }
+  stage();
+  const int nitems = nunits * iters;
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.f;
+  // item i -> (unit i / iters, chunk offset (i % iters) * U * 64)
+  DevMat N0 = A0, N1 = A1;
+  uint32_t nr0 = r0, nrmax = rmax;
+  auto next_desc = [&](int i) {
+    const int k = i / iters;
+    if (i % iters == 0) unit(k, N0, N1, nr0, nrmax);
+  };
+  auto finish = [&](int i) {
+    if (i % iters == iters - 1) {
+      float y[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        y[r] = wave_sum(acc[r]);
+        acc[r] = 0.f;
+      }
+      epi(i / iters, y);
+    }
+  };
+  for (int i = 0; i < nitems; i += 2) {
+    if (i + 1 < nitems) {
+      next_desc(i + 1);
+      mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, ((i + 1) % iters) * U * TALOS_WAVE, lane);
+    }
+    mv_compute<FMT, R, U>(b0, xs, xsum, nc, (i % iters) * U * TALOS_WAVE, lane, acc);
+    finish(i);
+    if (i + 1 >= nitems) break;
+    if (i + 2 < nitems) {
+      next_desc(i + 2);
+      mv_load<FMT, R, U, PAIR>(b0, N0, N1, nr0, nrmax, ((i + 2) % iters) * U * TALOS_WAVE, lane);
+    }
+    mv_compute<FMT, R, U>(b1, xs, xsum, nc, ((i + 1) % iters) * U * TALOS_WAVE, lane, acc);
+    finish(i + 1);
+  }
+}

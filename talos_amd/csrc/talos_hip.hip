@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -20,7 +21,7 @@
 #include <vector>
 
 #include "../../include/talos_hip.h"
-#include "kernels.h"
+#include "mega.h"
 
 namespace {
 
@@ -70,6 +71,23 @@ struct talos_hip_ctx {
   int32_t* h_tokens = nullptr;
 
   hipGraphExec_t graph[G_COUNT] = {nullptr, nullptr, nullptr, nullptr};
+  // TALOS_HIP_GRAPHS=0 enqueues the kernels directly instead of replaying a
+  // captured graph (same kernels; used under tracers that mishandle graphs).
+  bool use_graphs = true;
+
+  // Persistent one-kernel-per-token path (mega.h); TALOS_HIP_MEGA=0 turns it
+  // off.  mega_fn is the instantiation for this model's formats, or null.
+  bool allow_mega = true;
+  bool mega_ready = false;
+  const void* mega_fn = nullptr;
+  uint32_t mega_blocks = 0;
+  size_t mega_lds = 0;
+  MegaLayer* d_layers = nullptr;
+  uint32_t* d_sync = nullptr;
+  float* xb1 = nullptr;   // second residual base
+  float* o_out = nullptr;
+  float* d_out = nullptr;
+  MegaParams mp{};
 };
 
 namespace {
@@ -201,8 +219,35 @@ int need_norm(talos_hip_ctx* c, const std::string& name, size_t n, const float**
 
 int layout_need(uint32_t fmt) { return 1 << fmt_xlayout(fmt); }
 
+// Instantiate KERN<format, rows-per-unit, U> for the runtime (fmt, U) pair.
+#define TALOS_MV_U(KERN, F, U, ...)                                      \
+  do {                                                                   \
+    if ((U) >= 4) hipLaunchKernelGGL((KERN<F, mv_rows(F), 4>), __VA_ARGS__); \
+    else if ((U) == 2) hipLaunchKernelGGL((KERN<F, mv_rows(F), 2>), __VA_ARGS__); \
+    else hipLaunchKernelGGL((KERN<F, mv_rows(F), 1>), __VA_ARGS__);      \
+  } while (0)
+#define TALOS_MV_LAUNCH(KERN, fmt, U, ...)                                    \
+  do {                                                                        \
+    switch (fmt) {                                                            \
+      case TALOS_FMT_F32: TALOS_MV_U(KERN, TALOS_FMT_F32, U, __VA_ARGS__); break;   \
+      case TALOS_FMT_Q4_0: TALOS_MV_U(KERN, TALOS_FMT_Q4_0, U, __VA_ARGS__); break; \
+      case TALOS_FMT_Q8_0: TALOS_MV_U(KERN, TALOS_FMT_Q8_0, U, __VA_ARGS__); break; \
+      default: TALOS_MV_U(KERN, TALOS_FMT_Q6_K, U, __VA_ARGS__); break;       \
+    }                                                                         \
+  } while (0)
+
+template <uint32_t F>
+void set_lds_attr_fmt(int bytes) {
+  for (const void* k : {(const void*)k_qkv<F, mv_rows(F), 1>, (const void*)k_qkv<F, mv_rows(F), 2>,
+                        (const void*)k_qkv<F, mv_rows(F), 4>, (const void*)k_rows<F, mv_rows(F), 1>,
+                        (const void*)k_rows<F, mv_rows(F), 2>, (const void*)k_rows<F, mv_rows(F), 4>,
+                        (const void*)k_gateup<F, mv_rows(F), 1>, (const void*)k_gateup<F, mv_rows(F), 2>,
+                        (const void*)k_gateup<F, mv_rows(F), 4>})
+    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
 void plan(uint32_t units, uint32_t& upw, uint32_t& blocks) {
-  const uint32_t max_waves = 2048 * 4;
+  const uint32_t max_waves = 1024 * 4;
   upw = (units + max_waves - 1) / max_waves;
   if (upw == 0) upw = 1;
   const uint32_t waves = (units + upw - 1) / upw;
@@ -266,6 +311,9 @@ int layer_weights(talos_hip_ctx* c, uint32_t l, LayerW* w) {
       (rc = need_matrix(c, NM("ffn_down.weight"), n, cf.n_ff, &w->d)))
     return rc;
 #undef NM
+  if (w->k->type != w->q->type || w->v->type != w->q->type)
+    return fail(c, TALOS_ERR_DTYPE, "layer %u: attn_q/k/v must share one ggml type", l);
+  if (w->u->type != w->g->type) return fail(c, TALOS_ERR_DTYPE, "layer %u: ffn_gate/up must share one ggml type", l);
   return TALOS_OK;
 }
 
@@ -275,9 +323,10 @@ void enq_qkv(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
   P.m[0] = w.q->mat;
   P.m[1] = w.k->mat;
   P.m[2] = w.v->mat;
-  P.units[0] = n / 2;
-  P.units[1] = kvd / 2;
-  P.units[2] = kvd / 2;
+  const int R = mv_rows(w.q->mat.fmt);
+  P.units[0] = n / R;
+  P.units[1] = kvd / R;
+  P.units[2] = kvd / R;
   P.x = c->x;
   P.norm_w = w.an;
   P.eps = c->cfg.rms_eps;
@@ -292,7 +341,8 @@ void enq_qkv(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
   P.need = layout_need(w.q->mat.fmt) | layout_need(w.k->mat.fmt) | layout_need(w.v->mat.fmt);
   uint32_t blocks;
   plan(P.units[0] + P.units[1] + P.units[2], P.upw, blocks);
-  hipLaunchKernelGGL(k_qkv, dim3(blocks), dim3(256), stage_lds_bytes(n, P.need), c->stream, P);
+  TALOS_MV_LAUNCH(k_qkv, w.q->mat.fmt, mv_u(w.q->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, P.need),
+                  c->stream, P);
 }
 
 void enq_attn(talos_hip_ctx* c, uint32_t l) {
@@ -311,7 +361,7 @@ void enq_attn(talos_hip_ctx* c, uint32_t l) {
   A.max_chunk = c->max_chunk;
   A.scale = 1.0f / sqrtf((float)c->hd);
   const dim3 grid(c->cfg.n_head_kv, c->nsplit);
-  const size_t lds = attn_lds_bytes(c->hd, c->group, c->max_chunk);
+  const size_t lds = attn_lds_bytes(c->hd, c->group, c->nsplit, c->max_chunk);
   switch (c->hd / 16) {
     case 2: hipLaunchKernelGGL(k_attn<2>, grid, dim3(256), lds, c->stream, A); break;
     case 3: hipLaunchKernelGGL(k_attn<3>, grid, dim3(256), lds, c->stream, A); break;
@@ -330,11 +380,12 @@ void enq_resid(talos_hip_ctx* c, const DevWeight* w, const float* x, uint32_t n,
   R.n = n;
   R.out = out;
   R.accumulate = 1;
-  R.units = (uint32_t)((w->rows + 1) / 2);
+  R.units = (uint32_t)((w->rows + mv_rows(w->mat.fmt) - 1) / mv_rows(w->mat.fmt));
   R.need = layout_need(w->mat.fmt);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), stage_lds_bytes(n, R.need), c->stream, R);
+  TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
+                  c->stream, R);
 }
 
 void enq_gateup(talos_hip_ctx* c, const LayerW& w) {
@@ -346,11 +397,13 @@ void enq_gateup(talos_hip_ctx* c, const LayerW& w) {
   G.eps = c->cfg.rms_eps;
   G.n = c->cfg.n_embd;
   G.h = c->h;
-  G.units = c->cfg.n_ff;
+  const uint32_t pr = mv_rows(w.g->mat.fmt) / 2;
+  G.units = (c->cfg.n_ff + pr - 1) / pr;
   G.need = layout_need(w.g->mat.fmt) | layout_need(w.u->mat.fmt);
   uint32_t blocks;
   plan(G.units, G.upw, blocks);
-  hipLaunchKernelGGL(k_gateup, dim3(blocks), dim3(256), stage_lds_bytes(G.n, G.need), c->stream, G);
+  TALOS_MV_LAUNCH(k_gateup, w.g->mat.fmt, mv_u(w.g->mat.nchunk), dim3(blocks), dim3(256),
+                  stage_lds_bytes(G.n, G.need), c->stream, G);
 }
 
 void enq_output(talos_hip_ctx* c, const DevWeight* wout, const float* onorm) {
@@ -362,11 +415,12 @@ void enq_output(talos_hip_ctx* c, const DevWeight* wout, const float* onorm) {
   R.n = c->cfg.n_embd;
   R.out = c->logits;
   R.accumulate = 0;
-  R.units = (c->cfg.vocab_size + 1) / 2;
+  R.units = (c->cfg.vocab_size + mv_rows(wout->mat.fmt) - 1) / mv_rows(wout->mat.fmt);
   R.need = layout_need(wout->mat.fmt);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), stage_lds_bytes(R.n, R.need), c->stream, R);
+  TALOS_MV_LAUNCH(k_rows, wout->mat.fmt, mv_u(wout->mat.nchunk), dim3(blocks), dim3(256),
+                  stage_lds_bytes(R.n, R.need), c->stream, R);
 }
 
 // Enqueue one token step on the stream.
@@ -403,9 +457,20 @@ int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
   return TALOS_OK;
 }
 
+int mega_setup(talos_hip_ctx* c);
+
 int get_graph(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t* out) {
   int rc;
   if ((rc = alloc_acts(c))) return rc;
+  if ((rc = mega_setup(c))) return rc;
+  if (c->mega_fn) {
+    *out = nullptr;
+    return TALOS_OK;
+  }
+  if (!c->use_graphs) {
+    *out = nullptr;
+    return TALOS_OK;
+  }
   if (c->graph[kind]) {
     *out = c->graph[kind];
     return TALOS_OK;
@@ -427,6 +492,175 @@ int get_graph(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t* out) {
 }
 
 int set_state(talos_hip_ctx* c, uint32_t token, uint32_t pos);
+
+// After a step has synchronized with h_io holding the device state block:
+// a timed-out grid barrier in the persistent kernel leaves ST_ERR set.
+int check_device_err(talos_hip_ctx* c) {
+  if (c->h_io[ST_ERR] != 0)
+    return fail(c, TALOS_ERR_HIP, "persistent decode kernel: a grid barrier timed out (results invalid)");
+  return TALOS_OK;
+}
+
+// ---- persistent path
+
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL>
+const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl) {
+  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL)
+             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL>
+             : nullptr;
+}
+
+// The instantiations built into the library (the benchmark shapes); other
+// shape/format combinations use the multi-kernel graph path.
+const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl) {
+  const void* f = nullptr;
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8>(lf, of, un, uf, uo, dpl);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8>(lf, of, un, uf, uo, dpl);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8>(lf, of, un, uf, uo, dpl);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4>(lf, of, un, uf, uo, dpl);
+  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3>(lf, of, un, uf, uo, dpl);
+  return f;
+}
+
+// Prepare the persistent kernel for the resident weights; returns OK with
+// c->mega_fn == nullptr when this model has no instantiation.
+int mega_setup(talos_hip_ctx* c) {
+  if (c->mega_ready) return TALOS_OK;
+  c->mega_fn = nullptr;
+  if (!c->allow_mega) {
+    c->mega_ready = true;
+    return TALOS_OK;
+  }
+  int rc;
+  const auto& cf = c->cfg;
+  std::vector<MegaLayer> L(cf.n_layer);
+  uint32_t lf = 0;
+  for (uint32_t l = 0; l < cf.n_layer; ++l) {
+    LayerW w;
+    if ((rc = layer_weights(c, l, &w))) return rc;
+    const DevWeight* ms[] = {w.q, w.k, w.v, w.o, w.g, w.u, w.d};
+    if (l == 0) lf = w.q->mat.fmt;
+    for (const DevWeight* m : ms)
+      if (m->mat.fmt != lf) {
+        c->mega_ready = true;  // mixed formats: graph path
+        return TALOS_OK;
+      }
+    L[l] = MegaLayer{w.q->mat, w.k->mat, w.v->mat, w.o->mat, w.g->mat, w.u->mat, w.d->mat,
+                     w.an, w.fn, c->kc[l], c->vc[l]};
+  }
+  const DevWeight *wout, *emb;
+  const float* onorm;
+  if ((rc = need_matrix(c, "output.weight", cf.vocab_size, cf.n_embd, &wout)) ||
+      (rc = need_norm(c, "output_norm.weight", cf.n_embd, &onorm)) ||
+      (rc = need_matrix(c, "token_embd.weight", cf.vocab_size, cf.n_embd, &emb)))
+    return rc;
+  LayerW w0;
+  if ((rc = layer_weights(c, 0, &w0))) return rc;
+  const void* fn = mega_kernel_for(lf, wout->mat.fmt, mv_u(w0.q->mat.nchunk), std::min(mv_u(w0.d->mat.nchunk), 2),
+                                   mv_u(wout->mat.nchunk), (int)(c->hd / 16));
+  if (!fn) {
+    c->mega_ready = true;
+    return TALOS_OK;
+  }
+  int dev = cf.device;
+  hipDeviceProp_t prop;
+  HIPCHK(c, hipGetDeviceProperties(&prop, dev));
+  // Shapes the persistent kernel handles: batched staging of up to
+  // MEGA_STAGE_MAX floats, 128-position attention slices (at most nsplit).
+  if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX ||
+      (cf.context_length + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK > c->nsplit || c->hd % 16) {
+    c->mega_ready = true;
+    return TALOS_OK;
+  }
+  // LDS: x staging for the widest input, or the attention scratch.
+  const size_t st = stage_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), 3);
+  const size_t at = mega_attn_lds_floats(c->hd, c->group, c->nsplit) * 4;
+  c->mega_lds = std::max(st, at);
+  if (c->mega_lds > c->max_lds) {
+    c->mega_ready = true;
+    return TALOS_OK;
+  }
+  HIPCHK(c, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->mega_lds));
+  int per_cu = 0;
+  HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, MEGA_NT, c->mega_lds));
+  if (per_cu < 1) {
+    c->mega_ready = true;
+    return TALOS_OK;
+  }
+  c->mega_blocks = (uint32_t)prop.multiProcessorCount;
+  if (!c->d_layers) HIPCHK(c, hipMalloc(&c->d_layers, sizeof(MegaLayer) * cf.n_layer));
+  HIPCHK(c, hipMemcpy(c->d_layers, L.data(), sizeof(MegaLayer) * cf.n_layer, hipMemcpyHostToDevice));
+  if (!c->xb1) HIPCHK(c, hipMalloc(&c->xb1, (size_t)cf.n_embd * 4));
+  if (!c->o_out) HIPCHK(c, hipMalloc(&c->o_out, (size_t)cf.n_embd * 4));
+  if (!c->d_out) HIPCHK(c, hipMalloc(&c->d_out, (size_t)cf.n_embd * 4));
+  if (!c->d_sync) {
+    const size_t words = mega_sync_words(c->mega_blocks);
+    HIPCHK(c, hipMalloc(&c->d_sync, words * 4));
+    HIPCHK(c, hipMemset(c->d_sync, 0, words * 4));
+  }
+  MegaParams& P = c->mp;
+  P = MegaParams{};
+  P.layers = c->d_layers;
+  P.n_layer = cf.n_layer;
+  P.out_w = wout->mat;
+  P.out_norm = onorm;
+  P.embd = emb->mat;
+  P.n = cf.n_embd;
+  P.ff = cf.n_ff;
+  P.kv_dim = c->kv_dim;
+  P.hd = c->hd;
+  P.group = c->group;
+  P.n_kv = cf.n_head_kv;
+  P.vocab = cf.vocab_size;
+  P.eps = cf.rms_eps;
+  P.scale = 1.0f / sqrtf((float)c->hd);
+  P.rope = c->rope;
+  P.x = c->x;
+  P.xb[0] = c->x;
+  P.xb[1] = c->xb1;
+  P.o_out = c->o_out;
+  P.d_out = c->d_out;
+  P.q = c->q;
+  P.atty = c->atty;
+  P.h = c->h;
+  P.logits = c->logits;
+  P.hidden = c->hidden;
+  P.part = c->part;
+  P.count = c->count;
+  P.state = c->io;
+  P.tokens = c->tokens;
+  P.sync = c->d_sync;
+  P.nsplit = c->nsplit;
+  P.max_chunk = c->max_chunk;
+  c->mega_fn = fn;
+  c->mega_ready = true;
+  return TALOS_OK;
+}
+
+int mega_launch(talos_hip_ctx* c, GraphKind kind, uint64_t* timeline = nullptr) {
+  MegaParams P = c->mp;
+  P.timeline = timeline;
+  P.embed = kind == G_TOKEN || kind == G_GREEDY;
+  P.hidden_only = kind == G_HIDDEN;
+  P.argmax = kind == G_GREEDY ? 2 : (kind == G_TOKEN ? 1 : 0);
+  void* args[] = {&P};
+  HIPCHK(c, hipLaunchCooperativeKernel(c->mega_fn, dim3(c->mega_blocks), dim3(MEGA_NT), args,
+                                       (unsigned)c->mega_lds, c->stream));
+  return TALOS_OK;
+}
+
+// One token step: replay the captured graph, or enqueue the kernels.
+int run_step(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t g) {
+  if (c->mega_fn) return mega_launch(c, kind);
+  if (g) {
+    HIPCHK(c, hipGraphLaunch(g, c->stream));
+    return TALOS_OK;
+  }
+  int rc = enqueue_token(c, kind);
+  if (rc) return rc;
+  HIPCHK(c, hipGetLastError());
+  return TALOS_OK;
+}
 
 int check_ctx(talos_hip_ctx* c) {
   if (!c) return TALOS_ERR_ARG;
@@ -468,11 +702,18 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
 
   auto c = std::make_unique<talos_hip_ctx>();
   c->cfg = f;
+  const char* env = getenv("TALOS_HIP_GRAPHS");
+  c->use_graphs = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_MEGA");
+  c->allow_mega = !(env && env[0] == '0');
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;
-  uint32_t ns = (f.context_length + 127) / 128;
-  c->nsplit = ns < 1 ? 1 : (ns > 64 ? 64 : ns);
+  // Slices of TALOS_ATTN_CHUNK positions, at most 512 per KV head; the
+  // kernel uses ceil(seq / chunk) of them for the live sequence.  Past
+  // 512 * chunk positions the slices grow to ceil(ctx / 512).
+  uint32_t ns = (f.context_length + TALOS_ATTN_CHUNK - 1) / TALOS_ATTN_CHUNK;
+  c->nsplit = ns < 1 ? 1 : (ns > 512 ? 512 : ns);
   c->max_chunk = (f.context_length + c->nsplit - 1) / c->nsplit;
   hipError_t e = hipSetDevice(f.device);
   if (e != hipSuccess) return fail(nullptr, TALOS_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
@@ -483,8 +724,10 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   const size_t need_lds = stage_lds_bytes((int)std::max(f.n_embd, f.n_ff), 3);
   if (need_lds > c->max_lds)
     return fail(nullptr, TALOS_ERR_ARG, "n_ff %u needs %zu B of LDS, device has %zu", f.n_ff, need_lds, c->max_lds);
-  for (const void* k : {(const void*)k_qkv, (const void*)k_rows, (const void*)k_gateup})
-    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c->max_lds);
+  set_lds_attr_fmt<TALOS_FMT_F32>((int)c->max_lds);
+  set_lds_attr_fmt<TALOS_FMT_Q4_0>((int)c->max_lds);
+  set_lds_attr_fmt<TALOS_FMT_Q8_0>((int)c->max_lds);
+  set_lds_attr_fmt<TALOS_FMT_Q6_K>((int)c->max_lds);
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
     return fail(nullptr, TALOS_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
 
@@ -516,7 +759,8 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   for (auto& kv : c->weights) (void)hipFree(kv.second.mem);
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
-  void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope, c->mv_x, c->mv_out};
+  void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
+                 c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->xb1, c->o_out, c->d_out};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->h_io) (void)hipHostFree(c->h_io);
@@ -574,6 +818,7 @@ int talos_hip_upload_weight(talos_hip_ctx* c, const char* name, const void* byte
     c->weights.emplace(name, w);
   }
   destroy_graphs(c);  // graphs captured the old pointers
+  c->mega_ready = false;
   return TALOS_OK;
 }
 
@@ -591,11 +836,13 @@ static int forward_host(talos_hip_ctx* c, const float* x_embed, uint32_t pos, fl
   c->h_io[ST_POS] = (int32_t)pos;
   memcpy(c->h_io + 16, x_embed, (size_t)n * 4);
   HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64 + (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
-  HIPCHK(c, hipGraphLaunch(g, c->stream));
+  if ((rc = run_step(c, kind, g))) return rc;
   const size_t out_n = kind == G_HIDDEN ? n : c->cfg.vocab_size;
   HIPCHK(c, hipMemcpyAsync(c->h_out, kind == G_HIDDEN ? c->hidden : c->logits, out_n * 4, hipMemcpyDeviceToHost,
                            c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  if ((rc = check_device_err(c))) return rc;
   memcpy(out, c->h_out, out_n * 4);
   return TALOS_OK;
 }
@@ -630,11 +877,12 @@ int talos_hip_forward_token(talos_hip_ctx* c, uint32_t token, uint32_t pos, floa
   hipGraphExec_t g;
   if ((rc = get_graph(c, G_TOKEN, &g))) return rc;
   if ((rc = set_state(c, token, pos))) return rc;
-  HIPCHK(c, hipGraphLaunch(g, c->stream));
+  if ((rc = run_step(c, G_TOKEN, g))) return rc;
   if (logits)
     HIPCHK(c, hipMemcpyAsync(c->h_out, c->logits, (size_t)c->cfg.vocab_size * 4, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  if ((rc = check_device_err(c))) return rc;
   if (logits) memcpy(logits, c->h_out, (size_t)c->cfg.vocab_size * 4);
   if (argmax) *argmax = (uint32_t)c->h_io[ST_ARGMAX];
   return TALOS_OK;
@@ -652,10 +900,13 @@ int talos_hip_decode_greedy(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint
   hipGraphExec_t g;
   if ((rc = get_graph(c, G_GREEDY, &g))) return rc;
   if ((rc = set_state(c, token, pos))) return rc;
-  for (uint32_t s = 0; s < n_steps; ++s) HIPCHK(c, hipGraphLaunch(g, c->stream));
+  for (uint32_t s = 0; s < n_steps; ++s)
+    if ((rc = run_step(c, G_GREEDY, g))) return rc;
   if (n_steps)
     HIPCHK(c, hipMemcpyAsync(c->h_tokens, c->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, hipStreamSynchronize(c->stream));
+  if ((rc = check_device_err(c))) return rc;
   for (uint32_t s = 0; s < n_steps; ++s) tokens_out[s] = (uint32_t)c->h_tokens[s];
   return TALOS_OK;
 }
@@ -685,13 +936,13 @@ static int enqueue_matvec(talos_hip_ctx* c, const DevWeight* w, const float* d_x
   R.n = (uint32_t)w->cols;
   R.out = d_out;
   R.accumulate = 0;
-  R.units = (uint32_t)((w->rows + 1) / 2);
+  R.units = (uint32_t)((w->rows + mv_rows(w->mat.fmt) - 1) / mv_rows(w->mat.fmt));
   R.need = layout_need(w->mat.fmt);
   const size_t lds = stage_lds_bytes((int)w->cols, R.need);
   if (lds > c->max_lds) return fail(c, TALOS_ERR_SHAPE, "cols %zu needs %zu B of LDS", w->cols, lds);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  hipLaunchKernelGGL(k_rows, dim3(blocks), dim3(256), lds, c->stream, R);
+  TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), lds, c->stream, R);
   HIPCHK(c, hipGetLastError());
   return TALOS_OK;
 }
@@ -784,6 +1035,41 @@ int talos_hip_bench_kernel(talos_hip_ctx* c, const char* kind, uint32_t reps, fl
   *avg_us = ms * 1000.f / (float)reps;
   *bytes = b;
   return TALOS_OK;
+}
+
+int talos_hip_phase_timeline(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint64_t* marks, size_t cap,
+                             uint32_t* nblocks, uint32_t* slots, double* tick_ns) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!marks || !nblocks || !slots || !tick_ns) return fail(c, TALOS_ERR_ARG, "null argument");
+  if (pos >= c->cfg.context_length) return fail(c, TALOS_ERR_POS, "pos %u >= context_length", pos);
+  if (token >= c->cfg.vocab_size) return fail(c, TALOS_ERR_TOKEN, "token %u >= vocab_size", token);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_TOKEN, &g))) return rc;
+  if (!c->mega_fn) return fail(c, TALOS_ERR_ARG, "the persistent kernel is not in use for this model");
+  const size_t per = MEGA_TL_SLOTS(c->cfg.n_layer), n = per * c->mega_blocks;
+  *nblocks = c->mega_blocks;
+  *slots = (uint32_t)per;
+  if (cap < n) return fail(c, TALOS_ERR_ARG, "timeline needs %zu entries", n);
+  uint64_t* d = nullptr;
+  HIPCHK(c, hipMalloc(&d, n * 8));
+  HIPCHK(c, hipMemsetAsync(d, 0, n * 8, c->stream));
+  if ((rc = set_state(c, token, pos))) {
+    (void)hipFree(d);
+    return rc;
+  }
+  rc = mega_launch(c, G_TOKEN, d);
+  if (!rc) {
+    hipError_t e = hipMemcpyAsync(marks, d, n * 8, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) rc = fail(c, TALOS_ERR_HIP, "timeline copy: %s", hipGetErrorString(e));
+  }
+  (void)hipFree(d);
+  int rate_khz = 0;
+  (void)hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, c->cfg.device);
+  *tick_ns = rate_khz > 0 ? 1e6 / rate_khz : 10.0;
+  return rc;
 }
 
 void* talos_hip_stream(talos_hip_ctx* c) { return c ? (void*)c->stream : nullptr; }
