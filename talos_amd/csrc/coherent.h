@@ -1,11 +1,15 @@
 // coherent.h -- cross-workgroup data exchange inside one persistent kernel.
 //
 // The per-XCD L2 caches of MI355X are not coherent with each other while a
-// kernel runs.  Data one workgroup produces for another therefore moves with
-// agent-scope relaxed atomic loads/stores (global_load/store ... sc1), and a
-// producer waits for its stores to complete (s_waitcnt) before it signals.
-// Every wait is bounded: on timeout the kernel records an error and stops
-// waiting, so it always drains.
+// kernel runs.  Data one workgroup produces for another is written with
+// agent-scope relaxed atomic stores (global_store ... sc1, written through),
+// and the producer waits for its stores to complete (s_waitcnt) before it
+// signals.  A buffer written once per launch and read only after the barrier
+// that follows the write can then be read with ordinary cached loads: caches
+// are invalidated at kernel start, so no cache holds a copy of a line that
+// nobody read before it was written.  Words rewritten within a launch (flags,
+// counters) move with relaxed atomic loads (sc1).  Every wait is bounded: on
+// timeout the kernel records an error and stops waiting, so it always drains.
 #pragma once
 #include "device_common.h"
 
@@ -55,20 +59,31 @@ struct GridSync {
   uint32_t nblocks;
 };
 
-// Grid barrier with epoch `ep` (monotonic, compared modulo 2^32).  Every
-// block publishes its arrival; block 0 gathers all arrivals and publishes
-// `go`; the others wait for `go`.  All threads' prior coherent stores are
-// complete before the arrival is visible.
-__device__ __forceinline__ void grid_barrier(const GridSync& g, uint32_t ep) {
+// Shared flag: a wait timed out before this barrier, so it is skipped.
+__device__ __forceinline__ uint32_t& barrier_skip() {
+  __shared__ uint32_t timed_out;
+  return timed_out;
+}
+
+// Grid barrier with epoch `ep` (monotonic, compared modulo 2^32), in two
+// halves so that a block can issue independent loads between them.
+// grid_arrive: all threads' prior stores are complete, then the block
+// publishes its arrival.  grid_wait: block 0 gathers all arrivals and
+// publishes `go`; the others wait for `go`.  Vector memory operations of a
+// wave complete in issue order, so loads issued between the halves delay
+// that wave's view of the barrier; block 0 must not issue any.
+__device__ __forceinline__ void grid_arrive(const GridSync& g, uint32_t ep) {
   wait_mem();
   __syncthreads();
-  __shared__ uint32_t timed_out;
   if (threadIdx.x == 0) {
-    timed_out = ld_coh_u(g.err);
+    barrier_skip() = ld_coh_u(g.err);
     st_coh_u(g.flags + blockIdx.x * 16, ep);
   }
+}
+
+__device__ __forceinline__ void grid_wait(const GridSync& g, uint32_t ep) {
   __syncthreads();
-  const bool skip = timed_out != 0;
+  const bool skip = barrier_skip() != 0;
   if (blockIdx.x == 0) {
     if (!skip) {
       for (uint32_t w = threadIdx.x; w < g.nblocks; w += blockDim.x) {
@@ -93,4 +108,9 @@ __device__ __forceinline__ void grid_barrier(const GridSync& g, uint32_t ep) {
     }
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void grid_barrier(const GridSync& g, uint32_t ep) {
+  grid_arrive(g, ep);
+  grid_wait(g, ep);
 }

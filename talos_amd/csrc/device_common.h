@@ -1,7 +1,7 @@
 // device_common.h -- small device helpers shared by the decode kernels.
 //
 // Wavefront is 64 lanes (CDNA4).  All reductions are deterministic: fixed
-// butterfly order, no float atomics.
+// order, no float atomics.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,17 +17,56 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return (float)v;
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, TALOS_WAVE);
+// DPP lane moves (VOP_DPP controls of the CDNA ISA): quad permutes, row
+// (16-lane) rotates and row broadcasts.  Lanes a row mask leaves out take
+// `old`.
+#define DPP_QUAD_1032 0xB1
+#define DPP_QUAD_2301 0x4E
+#define DPP_ROW_ROR4 0x124
+#define DPP_ROW_ROR8 0x128
+#define DPP_ROW_BCAST15 0x142
+#define DPP_ROW_BCAST31 0x143
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over each quad of 4 lanes; every lane of the quad receives it.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp_f<DPP_QUAD_1032>(0.f, v);
+  v += dpp_f<DPP_QUAD_2301>(0.f, v);
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, TALOS_WAVE));
+// Sum over each row of 16 lanes; every lane of the row receives it.
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_f<DPP_QUAD_1032>(0.f, v);
+  v += dpp_f<DPP_QUAD_2301>(0.f, v);
+  v += dpp_f<DPP_ROW_ROR4>(0.f, v);
+  v += dpp_f<DPP_ROW_ROR8>(0.f, v);
   return v;
+}
+
+// Sum over the 64 lanes of a wave (row sums, then rows 0+1 into row 1,
+// 2+3 into row 3, then row 1 into rows 2-3; lane 63 holds the total);
+// every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  v += dpp_f<DPP_ROW_BCAST15, 0xA>(0.f, v);
+  v += dpp_f<DPP_ROW_BCAST31, 0xC>(0.f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v, v));
+  v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v, v));
+  v = fmaxf(v, dpp_f<DPP_ROW_ROR4>(v, v));
+  v = fmaxf(v, dpp_f<DPP_ROW_ROR8>(v, v));
+  v = fmaxf(v, dpp_f<DPP_ROW_BCAST15, 0xA>(v, v));
+  v = fmaxf(v, dpp_f<DPP_ROW_BCAST31, 0xC>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Sum over a block of `nwaves` waves through LDS scratch (>= nwaves floats).

@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
 }
 
 // --------------------------------------------------------------- k_rows --
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
 }
 
 // ------------------------------------------------------------- k_gateup --
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, true>(nunits, unit, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane);
+  mv_stream<FMT, R, U, true>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
 }
 
 // ---------------------------------------------------------------- k_attn --
@@ -319,10 +319,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
           float d = 0.f;
 #pragma unroll
           for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[h][i], kv[r][i], d);
-          d += __shfl_xor(d, 1, TALOS_WAVE);
-          d += __shfl_xor(d, 2, TALOS_WAVE);
-          d += __shfl_xor(d, 4, TALOS_WAVE);
-          d += __shfl_xor(d, 8, TALOS_WAVE);
+          d = row_sum16(d);
           if (tl < len && dl == 0) sc[h * mc + tl] = d * P.scale;
         }
       }

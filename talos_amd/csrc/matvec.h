@@ -238,8 +238,7 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int n, cons
       if (need1) *reinterpret_cast<f4*>(xs1 + xidx<1>(e4 * 4)) = v;
     }
     float s = (v.x + v.y) + (v.z + v.w);
-    s += __shfl_xor(s, 1, TALOS_WAVE);
-    s += __shfl_xor(s, 2, TALOS_WAVE);
+    s = quad_sum(s);
     if (e4 < n4 && (tid & 3) == 0) xsum[e4 >> 2] = s;
   }
   __syncthreads();

@@ -38,15 +38,13 @@ struct MegaParams {
   float eps, scale;
   const float* rope;
   float* x;        // layer-0 input when the host supplies the embedding
-  float* xb[2];    // residual base per layer parity (xb[0] == x)
-  float* o_out;    // o-projection output of the current layer
-  float* d_out;    // down-projection output of the current layer
-  float* q;
-  float* atty;
-  float* h;
+  float* act;      // per-layer activation slots (MEGA_ACT_*), lstride floats per layer
+  uint32_t np;     // n rounded up to 64: the stride of the n-sized slots
+  uint32_t lstride;
   float* logits;
   float* hidden;
-  float* part;
+  float* part;     // per-layer attention slice partials, pstride floats per layer
+  size_t pstride;
   uint32_t* count;
   int32_t* state;
   int32_t* tokens;
@@ -55,12 +53,33 @@ struct MegaParams {
   int embed;   // 1: x = embedding row of the state token, looked up on the device
   int hidden_only;
   int argmax;  // 0: none, 1: argmax into state, 2: argmax + advance (greedy loop)
+  int prefetch;  // issue each matvec phase's first weight loads before its barrier wait
   uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
 };
 
-// Phase timeline: per layer 11 marks (qkv staged/end, attention barrier/end,
-// o staged/end, gate-up staged/end, down staged/end, one spare), then head.
-#define MEGA_TL_PER_LAYER 11
+// Activation slots of one layer.  Every slot is written once per launch and
+// read only after the barrier that follows the write, so consumers read it
+// with ordinary cached loads (coherent.h).
+enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 3, MEGA_ACT_ATTY = 4, MEGA_ACT_H = 5 };
+static inline __host__ __device__ uint32_t mega_np(uint32_t n) { return (n + 63) & ~63u; }
+static inline __host__ __device__ uint32_t mega_lstride(uint32_t n, uint32_t ff) {
+  return 5 * mega_np(n) + mega_np(ff);
+}
+__device__ __forceinline__ float* mega_act(const MegaParams& P, uint32_t l, int slot) {
+  return P.act + (size_t)l * P.lstride + (size_t)slot * P.np;
+}
+// Residual base of layer l: the host-supplied x for layer 0 unless the
+// embedding is looked up on the device.
+__device__ __forceinline__ float* mega_base(const MegaParams& P, uint32_t l) {
+  return (l == 0 && !P.embed) ? P.x : mega_act(P, l, MEGA_ACT_BASE);
+}
+
+// Phase timeline: per layer 16 marks (qkv staged/end, attention barrier/end,
+// o staged/end, gate-up staged/end, down staged/end, one spare, then five
+// inside the block's first attention item: inputs loaded, softmax done, PV
+// reduced, slice published, item done), then head.
+#define MEGA_TL_PER_LAYER 16
+#define MEGA_TL_ATTN 11
 #define MEGA_TL_SLOTS(n_layer) ((n_layer) * MEGA_TL_PER_LAYER + 8)
 #define MEGA_MARK(P, slot)                                                                   \
   do {                                                                                       \
@@ -124,32 +143,31 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
       if (need & 2) *reinterpret_cast<f4*>(X.xs[1] + xidx<1>(e4 * 4)) = x;
     }
     float s = (x.x + x.y) + (x.z + x.w);
-    s += __shfl_xor(s, 1, TALOS_WAVE);
-    s += __shfl_xor(s, 2, TALOS_WAVE);
+    s = quad_sum(s);
     if (e4 < n4 && (tid & 3) == 0) X.xsum[e4 >> 2] = s;
   }
   __syncthreads();
 }
 
-// x[e..e+3] of one coherent array, of a + b, or of (a + b) + c: the residual
-// stream is kept as the layer's base plus the o-projection and down-
-// projection outputs, summed in the order of src/model/llama.rs:159-161,
-// 174-176.
-struct CohSrc {
+// x[e..e+3] of one array, of a + b, or of (a + b) + c: the residual stream
+// is kept as the layer's base plus the o-projection and down-projection
+// outputs, summed in the order of src/model/llama.rs:159-161, 174-176.
+__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+struct Src1 {
   const float* a;
-  __device__ __forceinline__ f4 operator()(int e) const { return ld_coh4(a + e); }
+  __device__ __forceinline__ f4 operator()(int e) const { return ld4(a + e); }
 };
-struct CohSrc2 {
+struct Src2 {
   const float *a, *b;
   __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = ld_coh4(a + e), y = ld_coh4(b + e);
+    const f4 x = ld4(a + e), y = ld4(b + e);
     return f4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
   }
 };
-struct CohSrc3 {
+struct Src3 {
   const float *a, *b, *c;
   __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = ld_coh4(a + e), y = ld_coh4(b + e), z = ld_coh4(c + e);
+    const f4 x = ld4(a + e), y = ld4(b + e), z = ld4(c + e);
     return f4{(x.x + y.x) + z.x, (x.y + y.y) + z.y, (x.z + y.z) + z.z, (x.w + y.w) + z.w};
   }
 };
@@ -171,20 +189,38 @@ __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t
 // MEGA_ATTN_CHUNK (src/model/llama.rs:139-155 for the GQA group of j).  All
 // K, V and q loads are issued together (one memory round trip); K uses 16
 // lanes per position (DPL dims each), V uses 4*DPL lanes per position (a
-// float4 each).  Data this step wrote (q, the K/V row at `pos`, slice
-// partials) is read coherently.  With nsp > 1 slices the last block to
-// finish for head j merges them in slice order.
+// float4 each).  q, the K/V row at `pos` and the slice partials are
+// written once per launch (coherent stores) and read after the barrier or
+// the slice counter that follows the write.  With nsp > 1 slices the last
+// block to finish for head j merges them in slice order.
 #define MEGA_ATTN_CHUNK 128
 
 static inline __host__ __device__ uint32_t mega_attn_ppr(uint32_t hd) { return MEGA_NT / (hd / 4); }
+// Positions per slice: ceil(seq * n_kv / nblocks) rounded up to 16, within
+// [16, MEGA_ATTN_CHUNK].  The slice count ceil(seq / chunk) is then at most
+// max(ceil(nblocks / n_kv), ceil(seq / MEGA_ATTN_CHUNK)).
+static inline __host__ __device__ int mega_attn_chunk(int seq, uint32_t n_kv, uint32_t nblocks) {
+  int c = (int)(((uint64_t)seq * n_kv + nblocks - 1) / nblocks);
+  c = (c + 15) & ~15;
+  return c < 16 ? 16 : (c > MEGA_ATTN_CHUNK ? MEGA_ATTN_CHUNK : c);
+}
+static inline uint32_t mega_attn_max_splits(uint32_t ctx, uint32_t n_kv, uint32_t nblocks) {
+  const uint32_t a = (nblocks + n_kv - 1) / n_kv, b = (ctx + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK;
+  return a > b ? a : b;
+}
 static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group, uint32_t nsplit) {
   const size_t ored = (size_t)mega_attn_ppr(hd) * group * hd, comb = 3 * (size_t)nsplit * group;
   return (size_t)group * hd + (size_t)group * MEGA_ATTN_CHUNK + (ored > comb ? ored : comb) + 64;
 }
 
 template <int DPL>
-__device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLayer& L, uint32_t j, int split,
-                                               int nsp, int pos, float* smem) {
+__device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLayer& L, const float* qv,
+                                               float* atty, float* part, uint32_t j, int split, int nsp, int chunk, int pos,
+                                               float* smem, int tls) {
+#define ATTN_MARK(k)                  \
+  do {                                \
+    if (tls >= 0) MEGA_MARK(P, tls + (k)); \
+  } while (0)
   constexpr int HD = 16 * DPL;            // head_dim
   constexpr int TPP = HD / 4;             // V threads per position
   constexpr int PPR = MEGA_NT / TPP;      // V positions per round
@@ -198,7 +234,6 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
   __shared__ int am_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int seq = pos + 1;
-  const int chunk = (seq + nsp - 1) / nsp;
   const int t0 = split * chunk;
   const int t1 = min(seq, t0 + chunk);
   const int len = max(0, t1 - t0);
@@ -212,9 +247,9 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
     const int tl = r * 32 + slot;
     const int t = t0 + (tl < len ? tl : 0);
     const float* kp = L.kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
-    if (t == pos) {
+    if (r * 32 >= len) {  // round past the slice (block-uniform)
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) kv[r][i] = ld_coh(kp + i);
+      for (int i = 0; i < DPL; ++i) kv[r][i] = 0.f;
     } else if constexpr (DPL % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < DPL; i += 4) {
@@ -237,31 +272,32 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
     const int tl = r * PPR + vp;
     if (vp < PPR && tl < len) {
       const float* p = L.vc + (size_t)(t0 + tl) * P.kv_dim + hoff + vd * 4;
-      vv[r] = t0 + tl == pos ? ld_coh4(p) : *reinterpret_cast<const f4*>(p);
+      vv[r] = ld4(p);
     } else {
       vv[r] = f4{0.f, 0.f, 0.f, 0.f};
     }
   }
   // q for the group's heads
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = ld_coh(P.q + (size_t)j * group * HD + i);
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = qv[(size_t)j * group * HD + i];
   __syncthreads();
+  ATTN_MARK(0);
 
   // scores
+  // (a 16-lane group is one DPP row)
+#pragma unroll 1
+  for (int h = 0; h < (int)group; ++h) {
+    float qr[DPL];
 #pragma unroll
-  for (int r = 0; r < KR; ++r) {
-    const int tl = r * 32 + slot;
+    for (int i = 0; i < DPL; ++i) qr[i] = qs[h * HD + dl * DPL + i];
 #pragma unroll
-    for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
-      if (h < (int)group) {
-        float d = 0.f;
+    for (int r = 0; r < KR; ++r) {
+      const int tl = r * 32 + slot;
+      if (r * 32 >= len) break;
+      float d = 0.f;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qs[h * HD + dl * DPL + i], kv[r][i], d);
-        d += __shfl_xor(d, 1, TALOS_WAVE);
-        d += __shfl_xor(d, 2, TALOS_WAVE);
-        d += __shfl_xor(d, 4, TALOS_WAVE);
-        d += __shfl_xor(d, 8, TALOS_WAVE);
-        if (tl < len && dl == 0) sc[h * MEGA_ATTN_CHUNK + tl] = d * P.scale;
-      }
+      for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[i], kv[r][i], d);
+      d = row_sum16(d);
+      if (tl < len && dl == 0) sc[h * MEGA_ATTN_CHUNK + tl] = d * P.scale;
     }
   }
   __syncthreads();
@@ -283,6 +319,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
     }
   }
   __syncthreads();
+  ATTN_MARK(1);
   // o[h][4vd..4vd+3] partial over this thread's positions
   if (vp < PPR) {
     f4 acc[TALOS_MAX_GROUP];
@@ -309,20 +346,22 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
       if (h < (int)group) *reinterpret_cast<f4*>(ored + ((size_t)vp * group + h) * HD + vd * 4) = acc[h];
   }
   __syncthreads();
+  ATTN_MARK(2);
 
   if (nsp == 1) {
     for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
       const uint32_t h = i / HD, dd = i % HD;
       float o = 0.f;
       for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
-      st_coh(P.atty + ((size_t)j * group + h) * HD + dd, o / lh[h]);
+      st_coh(atty + ((size_t)j * group + h) * HD + dd, o / lh[h]);
     }
     __syncthreads();
+    ATTN_MARK(4);
     return;
   }
 
   const size_t pstride = HD + 2;
-  float* mypart = P.part + ((size_t)j * P.nsplit + split) * group * pstride;
+  float* mypart = part + ((size_t)j * P.nsplit + split) * group * pstride;
   for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
     const uint32_t h = i / HD, dd = i % HD;
     float o = 0.f;
@@ -340,15 +379,16 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
     am_last = old == (uint32_t)nsp - 1;
   }
   __syncthreads();
+  ATTN_MARK(3);
   if (am_last) {
-    const float* parts = P.part + (size_t)j * P.nsplit * group * pstride;
+    const float* parts = part + (size_t)j * P.nsplit * group * pstride;
     float* cm = sc;  // reuses the score / reduction scratch
     float* cl = cm + nsp * group;
     float* cw = cl + nsp * group;
     for (int i = tid; i < nsp * (int)group; i += MEGA_NT) {
       const int s = i / (int)group, h = i % (int)group;
-      cm[i] = ld_coh(parts + ((size_t)s * group + h) * pstride + HD);
-      cl[i] = ld_coh(parts + ((size_t)s * group + h) * pstride + HD + 1);
+      cm[i] = parts[((size_t)s * group + h) * pstride + HD];
+      cl[i] = parts[((size_t)s * group + h) * pstride + HD + 1];
     }
     __syncthreads();
     if (tid < (int)group) {
@@ -370,16 +410,18 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
       for (; s + 4 <= nsp; s += 4) {
         float o4[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = ld_coh(parts + ((size_t)(s + r) * group + h) * pstride + dd);
+        for (int r = 0; r < 4; ++r) o4[r] = parts[((size_t)(s + r) * group + h) * pstride + dd];
 #pragma unroll
         for (int r = 0; r < 4; ++r) O = __builtin_fmaf(o4[r], cw[(s + r) * group + h], O);
       }
-      for (; s < nsp; ++s) O = __builtin_fmaf(ld_coh(parts + ((size_t)s * group + h) * pstride + dd), cw[s * group + h], O);
-      st_coh(P.atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
+      for (; s < nsp; ++s) O = __builtin_fmaf(parts[((size_t)s * group + h) * pstride + dd], cw[s * group + h], O);
+      st_coh(atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
   }
   __syncthreads();
+  ATTN_MARK(4);
+#undef ATTN_MARK
 }
 
 template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL>
@@ -403,13 +445,22 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   constexpr int RL = mv_rows(LF), RO = mv_rows(OF);
   constexpr int LL = MvT<LF>::L, LO = MvT<OF>::L;
   const int need_l = 1 << LL, need_o = 1 << LO;
+  // block 0 gathers the barrier arrivals, so it issues no loads before waiting
+  const bool pre = P.prefetch && blockIdx.x != 0;
   // this block's slice of the residual base it publishes each layer
   const int slice = (((int)P.n + (int)nb - 1) / (int)nb + 3) & ~3;
   const int pub_lo = (int)blockIdx.x * slice, pub_hi = pub_lo + slice;
+  auto arrive = [&] { grid_arrive(G, ep + 1); };
+  auto wait = [&] { grid_wait(G, ++ep); };
 
   for (uint32_t l = 0; l < P.n_layer; ++l) {
     const MegaLayer& L = P.layers[l];
-    float* base = P.xb[l & 1];
+    float* base = mega_base(P, l);
+    float* q = mega_act(P, l, MEGA_ACT_Q);
+    float* atty = mega_act(P, l, MEGA_ACT_ATTY);
+    float* o_out = mega_act(P, l, MEGA_ACT_O);
+    float* h = mega_act(P, l, MEGA_ACT_H);
+    float* d_out = mega_act(P, l, MEGA_ACT_D);
     // ---- qkv: rmsnorm(x) -> q/k/v -> RoPE -> q, K/V row at pos
     {
       const XStage X = carve_x(smem, P.n, need_l);
@@ -427,17 +478,20 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         r0 = p * RL;
         rmax = A0.rows;
       };
+      auto arr = [&] {
+        if (l > 0) arrive();
+      };
       auto stage = [&] {
         if (l > 0) {
-          grid_barrier(G, ++ep);
+          wait();
           // x = (base + attproj) + down of the previous layer; publish it
-          CohSrc3 src{P.xb[(l - 1) & 1], P.o_out, P.d_out};
+          Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
           mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
           mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
         } else {
-          CohSrc src{P.x};
+          Src1 src{P.x};
           mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
@@ -456,7 +510,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             const uint32_t i = (row % P.hd) / 2;
             const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
             const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
-            float* dst = s == 0 ? P.q + row : L.kc + (size_t)pos * P.kv_dim + row;
+            float* dst = s == 0 ? q + row : L.kc + (size_t)pos * P.kv_dim + row;
             st_coh(dst, y0 * c - y1 * sn);
             st_coh(dst + 1, y0 * sn + y1 * c);
           } else {
@@ -465,19 +519,28 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arr, stage, epi, X.xs[LL], X.xsum, lane,
+                                   pre && l > 0);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
     }
     // ---- attention over positions 0..pos
     {
       grid_barrier(G, ++ep);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 2);
+      // slices of 16..MEGA_ATTN_CHUNK positions, sized so that the items
+      // (KV head x slice) cover about one per block
       const int seq = pos + 1;
-      int nsp = (seq + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK;
-      if (nsp > (int)P.nsplit) nsp = (int)P.nsplit;
-      const uint32_t items = P.n_kv * (uint32_t)nsp;
-      for (uint32_t it = blockIdx.x; it < items; it += nb)
-        mega_attn_item<DPL>(P, L, it % P.n_kv, (int)(it / P.n_kv), nsp, pos, smem);
+      const int chunk = mega_attn_chunk(seq, P.n_kv, nb);
+      const int nsp = (seq + chunk - 1) / chunk;
+      if (nsp > (int)P.nsplit) {
+        if (threadIdx.x == 0) st_coh_u(G.err, 1u);  // host sized the partials too small
+      } else {
+        const uint32_t items = P.n_kv * (uint32_t)nsp;
+        float* part = P.part + (size_t)l * P.pstride;
+        for (uint32_t it = blockIdx.x; it < items; it += nb)
+          mega_attn_item<DPL>(P, L, q, atty, part, it % P.n_kv, (int)(it / P.n_kv), nsp, chunk, pos, smem,
+                              it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
+      }
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);
     }
     // ---- o-projection (the residual add happens where x is next read)
@@ -491,8 +554,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = L.o.rows;
       };
       auto stage = [&] {
-        grid_barrier(G, ++ep);
-        CohSrc src{P.atty};
+        wait();
+        Src1 src{atty};
         mega_stage(src, P.n, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
@@ -500,9 +563,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         if (lane != 0) return;
         const uint32_t r0 = (gw + (uint32_t)k * tw) * RL;
 #pragma unroll
-        for (int r = 0; r < RL; ++r) st_coh(P.o_out + r0 + r, y[r]);
+        for (int r = 0; r < RL; ++r) st_coh(o_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+                                   pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     }
     // ---- rmsnorm(base + attproj) + gate/up + SwiGLU
@@ -517,8 +581,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = L.g.rows;
       };
       auto stage = [&] {
-        grid_barrier(G, ++ep);
-        CohSrc2 src{base, P.o_out};
+        wait();
+        Src2 src{base, o_out};
         mega_stage(src, P.n, L.ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
@@ -529,11 +593,12 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         for (int r = 0; r < PR; ++r) {
           if (p0 + r < P.ff) {
             const float g = y[2 * r], u = y[2 * r + 1];
-            st_coh(P.h + p0 + r, (g / (1.0f + expf(-g))) * u);
+            st_coh(h + p0 + r, (g / (1.0f + expf(-g))) * u);
           }
         }
       };
-      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+                                  pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
     // ---- down-projection (2-row units keep the long rows' double buffer in
@@ -549,8 +614,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = L.d.rows;
       };
       auto stage = [&] {
-        grid_barrier(G, ++ep);
-        CohSrc src{P.h};
+        wait();
+        Src1 src{h};
         mega_stage(src, P.ff, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
       };
@@ -558,16 +623,20 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         if (lane != 0) return;
         const uint32_t r0 = (gw + (uint32_t)k * tw) * RD;
 #pragma unroll
-        for (int r = 0; r < RD; ++r) st_coh(P.d_out + r0 + r, y[r]);
+        for (int r = 0; r < RD; ++r) st_coh(d_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LL], X.xsum, lane);
+      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+                                   pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     }
   }
 
   // ---- head: final rmsnorm of (base + attproj) + down, then logits (+
   // argmax) or the hidden state
-  const float* last = P.xb[(P.n_layer - 1) & 1];
+  const uint32_t ll = P.n_layer - 1;
+  const float* last = mega_base(P, ll);
+  const float* last_o = mega_act(P, ll, MEGA_ACT_O);
+  const float* last_d = mega_act(P, ll, MEGA_ACT_D);
   __shared__ int32_t wk[MEGA_NW], wi[MEGA_NW];
   int32_t bk = INT32_MIN, bi = -1;
   if (P.hidden_only) {
@@ -575,13 +644,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     if (blockIdx.x == 0) {
       float ss = 0.f;
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (ld_coh(last + i) + ld_coh(P.o_out + i)) + ld_coh(P.d_out + i);
+        const float v = (last[i] + last_o[i]) + last_d[i];
         ss += v * v;
       }
       ss = block_sum(ss, smem, MEGA_NW);
       const float scale = 1.0f / sqrtf(ss / (float)P.n + P.eps);
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (ld_coh(last + i) + ld_coh(P.o_out + i)) + ld_coh(P.d_out + i);
+        const float v = (last[i] + last_o[i]) + last_d[i];
         P.hidden[i] = v * scale * P.out_norm[i];
       }
     }
@@ -595,8 +664,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       rmax = P.out_w.rows;
     };
     auto stage = [&] {
-      grid_barrier(G, ++ep);
-      CohSrc3 src{last, P.o_out, P.d_out};
+      wait();
+      Src3 src{last, last_o, last_d};
       mega_stage(src, P.n, P.out_norm, P.eps, true, X, need_o, nullptr, 0, 0);
       MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
     };
@@ -615,7 +684,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         }
       }
     };
-    mv_stream<OF, RO, UO, false>(mega_nunits(total, gw, tw), unit, stage, epi, X.xs[LO], X.xsum, lane);
+    mv_stream<OF, RO, UO, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LO], X.xsum, lane, pre);
     MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 1);
   }
   // per-block best, then the last block to finish reduces and advances state

@@ -3,8 +3,9 @@
 // A wave owns a run of "units" (R output rows of one matrix, or R/2 row pairs
 // of two matrices for gate/up) and walks each unit's columns in "items" of
 // U chunks per lane.  While it computes item i, the loads of item i+1 are in
-// flight; the first item's loads are issued before the block stages x into
-// LDS, so the HBM latency of the weights overlaps the rmsnorm/x setup.
+// flight; the first item's loads can be issued before the block waits for
+// its input and stages x into LDS, so the HBM latency of the weights
+// overlaps the grid barrier and the rmsnorm/x setup.
 // Weights are read once with 128-bit non-temporal loads; x comes from LDS and
 // is shared by the R rows of an item.
 #pragma once
@@ -130,12 +131,13 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const floa
 }
 
 // Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
-// unit of the wave (returns false past the end); epi(k, y) consumes the R
-// row results (every lane holds them).  `stage` is called once by every
-// thread of the block, after the first item's loads are issued.
-template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class StageFn, class EpiFn>
-__device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, StageFn stage, EpiFn epi, const float* xs,
-                                          const float* xsum, int lane) {
+// unit of the wave; epi(k, y) consumes the R row results (every lane holds
+// them).  `arrive` and `stage` are called once by every thread of the block;
+// with `pre` the first item's loads are issued between them (so they overlap
+// whatever `stage` waits for), otherwise after `stage`.
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class ArriveFn, class StageFn, class EpiFn>
+__device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
+                                          const float* xs, const float* xsum, int lane, bool pre) {
   MvBuf<FMT, R, U> b0, b1;
   int nc = 1, iters = 1;
   DevMat A0{}, A1{};
@@ -144,9 +146,11 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, StageFn stage
     unit(0, A0, A1, r0, rmax);
     nc = (int)A0.nchunk;
     iters = (nc + U * TALOS_WAVE - 1) / (U * TALOS_WAVE);
-    mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
   }
+  arrive();
+  if (pre && nunits > 0) mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
   stage();
+  if (!pre && nunits > 0) mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
   const int nitems = nunits * iters;
   float acc[R];
 #pragma unroll

@@ -84,9 +84,9 @@ struct talos_hip_ctx {
   size_t mega_lds = 0;
   MegaLayer* d_layers = nullptr;
   uint32_t* d_sync = nullptr;
-  float* xb1 = nullptr;   // second residual base
-  float* o_out = nullptr;
-  float* d_out = nullptr;
+  float* mact = nullptr;   // per-layer activation slots
+  float* mpart = nullptr;  // per-layer attention slice partials
+  bool mega_prefetch = true;  // TALOS_HIP_PREFETCH=0 turns cross-barrier weight prefetch off
   MegaParams mp{};
 };
 
@@ -566,15 +566,15 @@ int mega_setup(talos_hip_ctx* c) {
   hipDeviceProp_t prop;
   HIPCHK(c, hipGetDeviceProperties(&prop, dev));
   // Shapes the persistent kernel handles: batched staging of up to
-  // MEGA_STAGE_MAX floats, 128-position attention slices (at most nsplit).
-  if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX ||
-      (cf.context_length + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK > c->nsplit || c->hd % 16) {
+  // MEGA_STAGE_MAX floats, head_dim a multiple of 16.
+  if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX || c->hd % 16) {
     c->mega_ready = true;
     return TALOS_OK;
   }
   // LDS: x staging for the widest input, or the attention scratch.
   const size_t st = stage_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), 3);
-  const size_t at = mega_attn_lds_floats(c->hd, c->group, c->nsplit) * 4;
+  const uint32_t msplit = mega_attn_max_splits(cf.context_length, cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
+  const size_t at = mega_attn_lds_floats(c->hd, c->group, msplit) * 4;
   c->mega_lds = std::max(st, at);
   if (c->mega_lds > c->max_lds) {
     c->mega_ready = true;
@@ -590,9 +590,10 @@ int mega_setup(talos_hip_ctx* c) {
   c->mega_blocks = (uint32_t)prop.multiProcessorCount;
   if (!c->d_layers) HIPCHK(c, hipMalloc(&c->d_layers, sizeof(MegaLayer) * cf.n_layer));
   HIPCHK(c, hipMemcpy(c->d_layers, L.data(), sizeof(MegaLayer) * cf.n_layer, hipMemcpyHostToDevice));
-  if (!c->xb1) HIPCHK(c, hipMalloc(&c->xb1, (size_t)cf.n_embd * 4));
-  if (!c->o_out) HIPCHK(c, hipMalloc(&c->o_out, (size_t)cf.n_embd * 4));
-  if (!c->d_out) HIPCHK(c, hipMalloc(&c->d_out, (size_t)cf.n_embd * 4));
+  const uint32_t lstride = mega_lstride(cf.n_embd, cf.n_ff);
+  const size_t pstride = (size_t)cf.n_head_kv * msplit * c->group * (c->hd + 2);
+  if (!c->mact) HIPCHK(c, hipMalloc(&c->mact, (size_t)cf.n_layer * lstride * 4));
+  if (!c->mpart) HIPCHK(c, hipMalloc(&c->mpart, (size_t)cf.n_layer * pstride * 4));
   if (!c->d_sync) {
     const size_t words = mega_sync_words(c->mega_blocks);
     HIPCHK(c, hipMalloc(&c->d_sync, words * 4));
@@ -616,22 +617,20 @@ int mega_setup(talos_hip_ctx* c) {
   P.scale = 1.0f / sqrtf((float)c->hd);
   P.rope = c->rope;
   P.x = c->x;
-  P.xb[0] = c->x;
-  P.xb[1] = c->xb1;
-  P.o_out = c->o_out;
-  P.d_out = c->d_out;
-  P.q = c->q;
-  P.atty = c->atty;
-  P.h = c->h;
+  P.act = c->mact;
+  P.np = mega_np(cf.n_embd);
+  P.lstride = lstride;
   P.logits = c->logits;
   P.hidden = c->hidden;
-  P.part = c->part;
+  P.part = c->mpart;
+  P.pstride = pstride;
+  P.prefetch = c->mega_prefetch ? 1 : 0;
   P.count = c->count;
   P.state = c->io;
   P.tokens = c->tokens;
   P.sync = c->d_sync;
-  P.nsplit = c->nsplit;
-  P.max_chunk = c->max_chunk;
+  P.nsplit = msplit;
+  P.max_chunk = MEGA_ATTN_CHUNK;
   c->mega_fn = fn;
   c->mega_ready = true;
   return TALOS_OK;
@@ -706,6 +705,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->use_graphs = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_MEGA");
   c->allow_mega = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_PREFETCH");
+  c->mega_prefetch = !(env && env[0] == '0');
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;
@@ -760,7 +761,7 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
-                 c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->xb1, c->o_out, c->d_out};
+                 c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->h_io) (void)hipHostFree(c->h_io);
