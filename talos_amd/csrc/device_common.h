@@ -11,6 +11,25 @@
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
+// Pointers read from memory (rather than kernel arguments) are generic, and
+// generic accesses compile to flat instructions, which also count against
+// lgkmcnt: every LDS wait would then also wait for them.  These casts state
+// that an address is in global memory, so the access is a global_* one.
+#define TALOS_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const TALOS_GLOBAL T* gptr(const T* p) {
+  return (const TALOS_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ TALOS_GLOBAL T* gptr(T* p) {
+  return (TALOS_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *gptr(p);
+}
+__device__ __forceinline__ f4 gld4(const float* p) { return gld(reinterpret_cast<const f4*>(p)); }
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   _Float16 v;
   __builtin_memcpy(&v, &h, 2);

@@ -32,32 +32,13 @@ __device__ __forceinline__ f4 lds4(const float* xs, int i) {
   return *reinterpret_cast<const f4*>(xs + i);
 }
 
+// 16 weight bytes, read once: non-temporal global load.
 __device__ __forceinline__ u4 ldg4(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
+  return __builtin_nontemporal_load(gptr(reinterpret_cast<const u4*>(p)));
 }
 
-// ---- per-format chunk dots.  Each adds the dot of one chunk of row A (and
-// row B when `two`) with x onto accA / accB.
-
-__device__ __forceinline__ void chunk_f32(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                          bool two, const float* xs, int c, float& accA, float& accB) {
-  const f4 x = lds4(xs, xidx<0>(c * 4));
-  const size_t stride = (size_t)A.nchunk * 16;  // rows padded to a multiple of 16 floats
-  const u4 wa = ldg4(A.q + ra * stride + (size_t)c * 16);
-  f4 fa = __builtin_bit_cast(f4, wa);
-  accA = __builtin_fmaf(fa.x, x.x, accA);
-  accA = __builtin_fmaf(fa.y, x.y, accA);
-  accA = __builtin_fmaf(fa.z, x.z, accA);
-  accA = __builtin_fmaf(fa.w, x.w, accA);
-  if (two) {
-    const u4 wb = ldg4(B.q + rb * stride + (size_t)c * 16);
-    f4 fb = __builtin_bit_cast(f4, wb);
-    accB = __builtin_fmaf(fb.x, x.x, accB);
-    accB = __builtin_fmaf(fb.y, x.y, accB);
-    accB = __builtin_fmaf(fb.z, x.z, accB);
-    accB = __builtin_fmaf(fb.w, x.w, accB);
-  }
-}
+// ---- per-format block dots: the dot of one block's raw (unsigned) quants
+// with x, minus the quant offset folded in through the x group sums.
 
 __device__ __forceinline__ float q4_block_dot(u4 q, const f4* x, float xs8) {
   float s = 0.f;
@@ -73,26 +54,6 @@ __device__ __forceinline__ float q4_block_dot(u4 q, const f4* x, float xs8) {
   return (s + t) - xs8;
 }
 
-__device__ __forceinline__ void chunk_q4_0(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                           bool two, const float* xs, const float* xsum, int c,
-                                           float& accA, float& accB) {
-  const size_t nc = A.nchunk;
-  const u4 qa = ldg4(A.q + (ra * nc + c) * 16);
-  const float da = f16_to_f32(A.d[ra * nc + c]);
-  u4 qb;
-  float db = 0.f;
-  if (two) {
-    qb = ldg4(B.q + (rb * nc + c) * 16);
-    db = f16_to_f32(B.d[rb * nc + c]);
-  }
-  f4 x[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = lds4(xs, xidx<0>(c * 32 + i * 4));
-  const float xs8 = 8.f * (xsum[2 * c] + xsum[2 * c + 1]);
-  accA = __builtin_fmaf(da, q4_block_dot(qa, x, xs8), accA);
-  if (two) accB = __builtin_fmaf(db, q4_block_dot(qb, x, xs8), accB);
-}
-
 __device__ __forceinline__ float q8_block_dot(u4 q0, u4 q1, const f4* x, float xs128) {
   float s = 0.f, t = 0.f;
   s = dot_ub4(q0.x, x[0], s);
@@ -104,29 +65,6 @@ __device__ __forceinline__ float q8_block_dot(u4 q0, u4 q1, const f4* x, float x
   s = dot_ub4(q1.z, x[6], s);
   t = dot_ub4(q1.w, x[7], t);
   return (s + t) - xs128;
-}
-
-__device__ __forceinline__ void chunk_q8_0(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                           bool two, const float* xs, const float* xsum, int c,
-                                           float& accA, float& accB) {
-  const size_t nc = A.nchunk;
-  const uint8_t* pa = A.q + (ra * nc + c) * 32;
-  const u4 qa0 = ldg4(pa), qa1 = ldg4(pa + 16);
-  const float da = f16_to_f32(A.d[ra * nc + c]);
-  u4 qb0, qb1;
-  float db = 0.f;
-  if (two) {
-    const uint8_t* pb = B.q + (rb * nc + c) * 32;
-    qb0 = ldg4(pb);
-    qb1 = ldg4(pb + 16);
-    db = f16_to_f32(B.d[rb * nc + c]);
-  }
-  f4 x[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = lds4(xs, xidx<0>(c * 32 + i * 4));
-  const float xs128 = 128.f * (xsum[2 * c] + xsum[2 * c + 1]);
-  accA = __builtin_fmaf(da, q8_block_dot(qa0, qa1, x, xs128), accA);
-  if (two) accB = __builtin_fmaf(db, q8_block_dot(qb0, qb1, x, xs128), accB);
 }
 
 // One quarter super-block of Q6_K: byte j of the three planes yields the four
@@ -155,38 +93,6 @@ __device__ __forceinline__ float q6_chunk_dot(u4 a, u4 b, u4 h, uint32_t scw, co
   t = __builtin_fmaf(s2, r2 - xsr[2], t);
   t = __builtin_fmaf(s3, r3 - xsr[3], t);
   return t;
-}
-
-__device__ __forceinline__ void chunk_q6_k(const DevMat& A, uint32_t ra, const DevMat& B, uint32_t rb,
-                                           bool two, const float* xs, const float* xsum, int c,
-                                           float& accA, float& accB) {
-  const size_t nc = A.nchunk;
-  const uint8_t* pa = A.q + ra * nc * 48 + (size_t)c * 16;
-  const u4 a0 = ldg4(pa), a1 = ldg4(pa + nc * 16), a2 = ldg4(pa + nc * 32);
-  const uint32_t sca = A.sc[ra * nc + c];
-  const float da = f16_to_f32(A.d[ra * (nc >> 2) + (c >> 2)]);
-  u4 b0, b1, b2;
-  uint32_t scb = 0;
-  float db = 0.f;
-  if (two) {
-    const uint8_t* pb = B.q + rb * nc * 48 + (size_t)c * 16;
-    b0 = ldg4(pb);
-    b1 = ldg4(pb + nc * 16);
-    b2 = ldg4(pb + nc * 32);
-    scb = B.sc[rb * nc + c];
-    db = f16_to_f32(B.d[rb * (nc >> 2) + (c >> 2)]);
-  }
-  const int base = (c >> 2) * 256 + ((c >> 1) & 1) * 128 + (c & 1) * 16;
-  f4 x[16];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) x[r * 4 + k] = lds4(xs, xidx<1>(base + r * 32 + k * 4));
-  float xsr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) xsr[r] = 32.f * xsum[(base + r * 32) >> 4];
-  accA = __builtin_fmaf(da, q6_chunk_dot(a0, a1, a2, sca, x, xsr), accA);
-  if (two) accB = __builtin_fmaf(db, q6_chunk_dot(b0, b1, b2, scb, x, xsr), accB);
 }
 
 // Stage n floats of x into LDS (layouts flagged by need0/need1) plus the

@@ -57,6 +57,21 @@ struct MegaParams {
   uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
 };
 
+// Read-only tables read through the constant address space compile to
+// scalar loads.
+#define TALOS_CONST __attribute__((address_space(4)))
+__device__ __forceinline__ DevMat const_mat(const TALOS_CONST DevMat* p) {
+  DevMat m;
+  m.q = p->q;
+  m.d = p->d;
+  m.sc = p->sc;
+  m.rows = p->rows;
+  m.cols = p->cols;
+  m.fmt = p->fmt;
+  m.nchunk = p->nchunk;
+  return m;
+}
+
 // Activation slots of one layer.  Every slot is written once per launch and
 // read only after the barrier that follows the write, so consumers read it
 // with ordinary cached loads (coherent.h).
@@ -133,7 +148,7 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
     if (e4 < n4) {
       if (pub && e4 < nr && e4 * 4 >= pub_lo && e4 * 4 < pub_hi) st_coh4(pub + e4 * 4, x);
       if (norm && e4 < nr) {
-        const f4 ww = *reinterpret_cast<const f4*>(w + e4 * 4);
+        const f4 ww = gld4(w + e4 * 4);
         x.x = x.x * scale * ww.x;
         x.y = x.y * scale * ww.y;
         x.z = x.z * scale * ww.z;
@@ -152,22 +167,21 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
 // x[e..e+3] of one array, of a + b, or of (a + b) + c: the residual stream
 // is kept as the layer's base plus the o-projection and down-projection
 // outputs, summed in the order of src/model/llama.rs:159-161, 174-176.
-__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 struct Src1 {
   const float* a;
-  __device__ __forceinline__ f4 operator()(int e) const { return ld4(a + e); }
+  __device__ __forceinline__ f4 operator()(int e) const { return gld4(a + e); }
 };
 struct Src2 {
   const float *a, *b;
   __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = ld4(a + e), y = ld4(b + e);
+    const f4 x = gld4(a + e), y = gld4(b + e);
     return f4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
   }
 };
 struct Src3 {
   const float *a, *b, *c;
   __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = ld4(a + e), y = ld4(b + e), z = ld4(c + e);
+    const f4 x = gld4(a + e), y = gld4(b + e), z = gld4(c + e);
     return f4{(x.x + y.x) + z.x, (x.y + y.y) + z.y, (x.z + y.z) + z.z, (x.w + y.w) + z.w};
   }
 };
@@ -214,7 +228,7 @@ static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group, uint32_t 
 }
 
 template <int DPL>
-__device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLayer& L, const float* qv,
+__device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float* kc, const float* vc, const float* qv,
                                                float* atty, float* part, uint32_t j, int split, int nsp, int chunk, int pos,
                                                float* smem, int tls) {
 #define ATTN_MARK(k)                  \
@@ -246,14 +260,14 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
   for (int r = 0; r < KR; ++r) {
     const int tl = r * 32 + slot;
     const int t = t0 + (tl < len ? tl : 0);
-    const float* kp = L.kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
+    const float* kp = kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
     if (r * 32 >= len) {  // round past the slice (block-uniform)
 #pragma unroll
       for (int i = 0; i < DPL; ++i) kv[r][i] = 0.f;
     } else if constexpr (DPL % 4 == 0) {
 #pragma unroll
       for (int i = 0; i < DPL; i += 4) {
-        const f4 v = *reinterpret_cast<const f4*>(kp + i);
+        const f4 v = gld4(kp + i);
         kv[r][i] = v.x;
         kv[r][i + 1] = v.y;
         kv[r][i + 2] = v.z;
@@ -261,7 +275,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) kv[r][i] = kp[i];
+      for (int i = 0; i < DPL; ++i) kv[r][i] = gld(kp + i);
     }
   }
   // V: TPP threads per position, a float4 each
@@ -271,14 +285,14 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
   for (int r = 0; r < VR; ++r) {
     const int tl = r * PPR + vp;
     if (vp < PPR && tl < len) {
-      const float* p = L.vc + (size_t)(t0 + tl) * P.kv_dim + hoff + vd * 4;
-      vv[r] = ld4(p);
+      const float* p = vc + (size_t)(t0 + tl) * P.kv_dim + hoff + vd * 4;
+      vv[r] = gld4(p);
     } else {
       vv[r] = f4{0.f, 0.f, 0.f, 0.f};
     }
   }
   // q for the group's heads
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = qv[(size_t)j * group * HD + i];
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)j * group * HD + i);
   __syncthreads();
   ATTN_MARK(0);
 
@@ -387,8 +401,8 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
     float* cw = cl + nsp * group;
     for (int i = tid; i < nsp * (int)group; i += MEGA_NT) {
       const int s = i / (int)group, h = i % (int)group;
-      cm[i] = parts[((size_t)s * group + h) * pstride + HD];
-      cl[i] = parts[((size_t)s * group + h) * pstride + HD + 1];
+      cm[i] = gld(parts + ((size_t)s * group + h) * pstride + HD);
+      cl[i] = gld(parts + ((size_t)s * group + h) * pstride + HD + 1);
     }
     __syncthreads();
     if (tid < (int)group) {
@@ -410,11 +424,11 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const MegaLa
       for (; s + 4 <= nsp; s += 4) {
         float o4[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = parts[((size_t)(s + r) * group + h) * pstride + dd];
+        for (int r = 0; r < 4; ++r) o4[r] = gld(parts + ((size_t)(s + r) * group + h) * pstride + dd);
 #pragma unroll
         for (int r = 0; r < 4; ++r) O = __builtin_fmaf(o4[r], cw[(s + r) * group + h], O);
       }
-      for (; s < nsp; ++s) O = __builtin_fmaf(parts[((size_t)s * group + h) * pstride + dd], cw[s * group + h], O);
+      for (; s < nsp; ++s) O = __builtin_fmaf(gld(parts + ((size_t)s * group + h) * pstride + dd), cw[s * group + h], O);
       st_coh(atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
@@ -453,8 +467,12 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   auto arrive = [&] { grid_arrive(G, ep + 1); };
   auto wait = [&] { grid_wait(G, ++ep); };
 
+  // The layer table is read-only for the launch: reading it through the
+  // constant address space gives scalar loads.
+  typedef const TALOS_CONST MegaLayer* LayerTab;
+  const LayerTab layer_tab = (LayerTab)P.layers;
   for (uint32_t l = 0; l < P.n_layer; ++l) {
-    const MegaLayer& L = P.layers[l];
+    const auto LP = layer_tab + l;  // fields are copied out where used
     float* base = mega_base(P, l);
     float* q = mega_act(P, l, MEGA_ACT_Q);
     float* atty = mega_act(P, l, MEGA_ACT_ATTY);
@@ -473,7 +491,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         int s;
         uint32_t p;
         seg(gw + (uint32_t)k * tw, s, p);
-        A0 = pick3(L.q, L.k, L.v, s);
+        A0 = s == 0 ? const_mat(&LP->q) : (s == 1 ? const_mat(&LP->k) : const_mat(&LP->v));
         A1 = A0;
         r0 = p * RL;
         rmax = A0.rows;
@@ -486,13 +504,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           wait();
           // x = (base + attproj) + down of the previous layer; publish it
           Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
         } else {
           Src1 src{P.x};
-          mega_stage(src, P.n, L.attn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -510,12 +528,12 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             const uint32_t i = (row % P.hd) / 2;
             const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
             const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
-            float* dst = s == 0 ? q + row : L.kc + (size_t)pos * P.kv_dim + row;
+            float* dst = s == 0 ? q + row : LP->kc + (size_t)pos * P.kv_dim + row;
             st_coh(dst, y0 * c - y1 * sn);
             st_coh(dst + 1, y0 * sn + y1 * c);
           } else {
-            st_coh(L.vc + (size_t)pos * P.kv_dim + row, y0);
-            st_coh(L.vc + (size_t)pos * P.kv_dim + row + 1, y1);
+            st_coh(LP->vc + (size_t)pos * P.kv_dim + row, y0);
+            st_coh(LP->vc + (size_t)pos * P.kv_dim + row + 1, y1);
           }
         }
       };
@@ -538,7 +556,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         const uint32_t items = P.n_kv * (uint32_t)nsp;
         float* part = P.part + (size_t)l * P.pstride;
         for (uint32_t it = blockIdx.x; it < items; it += nb)
-          mega_attn_item<DPL>(P, L, q, atty, part, it % P.n_kv, (int)(it / P.n_kv), nsp, chunk, pos, smem,
+          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, part, it % P.n_kv, (int)(it / P.n_kv), nsp, chunk, pos, smem,
                               it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
       }
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);
@@ -548,10 +566,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       const XStage X = carve_x(smem, P.n, need_l);
       const uint32_t total = P.n / RL;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
-        A0 = L.o;
-        A1 = L.o;
+        A0 = const_mat(&LP->o);
+        A1 = A0;
         r0 = (gw + (uint32_t)k * tw) * RL;
-        rmax = L.o.rows;
+        rmax = LP->o.rows;
       };
       auto stage = [&] {
         wait();
@@ -575,15 +593,15 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       constexpr int PR = RL / 2;
       const uint32_t total = (P.ff + PR - 1) / PR;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
-        A0 = L.g;
-        A1 = L.u;
+        A0 = const_mat(&LP->g);
+        A1 = const_mat(&LP->u);
         r0 = (gw + (uint32_t)k * tw) * PR;
-        rmax = L.g.rows;
+        rmax = LP->g.rows;
       };
       auto stage = [&] {
         wait();
         Src2 src{base, o_out};
-        mega_stage(src, P.n, L.ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+        mega_stage(src, P.n, LP->ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -608,10 +626,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       const XStage X = carve_x(smem, P.ff, need_l);
       const uint32_t total = P.n / RD;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
-        A0 = L.d;
-        A1 = L.d;
+        A0 = const_mat(&LP->d);
+        A1 = A0;
         r0 = (gw + (uint32_t)k * tw) * RD;
-        rmax = L.d.rows;
+        rmax = LP->d.rows;
       };
       auto stage = [&] {
         wait();
@@ -644,13 +662,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     if (blockIdx.x == 0) {
       float ss = 0.f;
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (last[i] + last_o[i]) + last_d[i];
+        const float v = (gld(last + i) + gld(last_o + i)) + gld(last_d + i);
         ss += v * v;
       }
       ss = block_sum(ss, smem, MEGA_NW);
       const float scale = 1.0f / sqrtf(ss / (float)P.n + P.eps);
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (last[i] + last_o[i]) + last_d[i];
+        const float v = (gld(last + i) + gld(last_o + i)) + gld(last_d + i);
         P.hidden[i] = v * scale * P.out_norm[i];
       }
     }

@@ -57,18 +57,18 @@ __device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, c
         B.q[i][u][0] = ldg4(M.q + ci * 16);
       } else if (FMT == TALOS_FMT_Q4_0) {
         B.q[i][u][0] = ldg4(M.q + ci * 16);
-        B.a[i][u] = M.d[ci];
+        B.a[i][u] = gld(M.d + ci);
       } else if (FMT == TALOS_FMT_Q8_0) {
         B.q[i][u][0] = ldg4(M.q + ci * 32);
         B.q[i][u][MvT<FMT>::QW - 1] = ldg4(M.q + ci * 32 + 16);
-        B.a[i][u] = M.d[ci];
+        B.a[i][u] = gld(M.d + ci);
       } else {
         const uint8_t* p = M.q + (size_t)row * nc * 48 + (size_t)c * 16;
         B.q[i][u][0] = ldg4(p);
         B.q[i][u][MvT<FMT>::QW > 1 ? 1 : 0] = ldg4(p + (size_t)nc * 16);
         B.q[i][u][MvT<FMT>::QW - 1] = ldg4(p + (size_t)nc * 32);
-        B.a[i][u] = M.sc[ci];
-        B.b[i][u] = M.d[(size_t)row * (nc >> 2) + (c >> 2)];
+        B.a[i][u] = gld(M.sc + ci);
+        B.b[i][u] = gld(M.d + (size_t)row * (nc >> 2) + (c >> 2));
       }
     }
   }
