@@ -6,15 +6,16 @@ heads (head_dim 128), 8 KV heads, FFN 14336, vocab 32000, RoPE theta 1e6 --
 with seeded N(0, 0.02) weights quantized to Q4_0 (output.weight Q6_K), KV
 cache sized to 4096 positions, a random 32-token prompt and then greedy
 decode steps.  A step is one token's whole forward (embedding lookup, 32
-layers, output projection, argmax) replayed as one hipGraph with the token,
-position, weights and KV already resident in HBM.
+layers, output projection, argmax), which runs as one persistent kernel
+launch with the token, position, weights and KV already resident in HBM.
 
 Prints one JSON line.  `value` is decode tokens/s over exactly --steps timed
-steps.  `roofline` is the dominant kernel (the fused rmsnorm + gate/up +
-SwiGLU matvec) timed with HIP events on its stream; `token_roofline` is the
-whole step against the weights + KV byte floor.  `cpu_baseline` is the
-oracle (a C restatement of the reference's CPU forward) on a bounded sample
-of the same workload, whose greedy tokens are also compared with the GPU's.
+steps.  `roofline` is that kernel (the whole decode step) timed with HIP
+events on its stream at the middle position of the timed run: algorithmic
+bytes per step (weights once, K/V read and written, logits) over the mean
+step time.  `cpu_baseline` is the oracle (a C restatement of the
+reference's CPU forward) on a bounded sample of the same model, whose greedy
+tokens are also compared with the GPU's.
 """
 from __future__ import annotations
 
@@ -30,6 +31,8 @@ if ROOT not in sys.path:
 
 METRIC = "decode tok/s batch-1 @7B-shape Q4_0; matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
+PHASES = ["qkv_work", "attn_barrier", "attn_work", "o_barrier_stage", "o_work", "gateup_barrier_stage",
+          "gateup_work", "down_barrier_stage", "down_work", "next_layer_barrier_stage"]
 
 
 def host_threads() -> int:
@@ -42,8 +45,41 @@ def host_threads() -> int:
         return os.cpu_count() or 1
 
 
+TRAFFIC_FILE = os.path.join("profiles", "k_mega_7b_q4_pmc_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode step, from the rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE runs summarized in TRAFFIC_FILE (scaled by a copy
+    kernel of known size), or None."""
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
+            for line in f:
+                if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
+                    return int(line.split("=")[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def phase_breakdown(tl, n_layer: int, per_layer: int = 16) -> dict:
+    """Mean microseconds per layer of each phase of one step, from the
+    latest workgroup's mark at each phase boundary."""
+    import numpy as np
+    mx = tl.max(axis=0)
+    seg = {k: [] for k in PHASES}
+    for l in range(n_layer):
+        b = l * per_layer
+        d = [mx[b + i + 1] - mx[b + i] for i in range(9)]
+        for k, v in zip(PHASES[:9], d):
+            seg[k].append(v)
+        if l + 1 < n_layer:
+            seg[PHASES[9]].append(mx[b + per_layer] - mx[b + 9])
+    return {k: round(float(np.mean(v)) / 1e3, 2) for k, v in seg.items() if v}
 
 
 def main() -> int:
@@ -51,7 +87,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128, help="timed decode steps (tokens)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before timing")
-    ap.add_argument("--cpu-tokens", type=int, default=8, help="decode tokens in the CPU baseline sample")
+    ap.add_argument("--cpu-prompt", type=int, default=8, help="prompt tokens of the CPU baseline sample")
+    ap.add_argument("--cpu-tokens", type=int, default=32, help="greedy decode tokens of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -67,14 +104,14 @@ def main() -> int:
     wl = configs.mistral7b_q4(ctx=4096)
     spec = wl.spec
     P = wl.prompt_len
-    if P + max(args.steps, args.warmup) > spec.context_length:
+    if P + args.warmup + args.steps > spec.context_length:
         print(f"--steps/--warmup exceed the KV capacity ({spec.context_length - P})", file=sys.stderr)
         return 2
     nthreads = host_threads()
     log(f"generating {wl.name} (seed {spec.seed}) with {nthreads} threads")
     t = time.perf_counter()
     model = T.Model.synth(spec, nthreads=nthreads)
-    log(f"  generated in {time.perf_counter() - t:.1f}s; uploading + first graph")
+    log(f"  generated in {time.perf_counter() - t:.1f}s")
     prompt = [int(x) for x in np.random.default_rng(spec.seed + 1).integers(0, spec.vocab_size, P)]
 
     def prefill() -> int:
@@ -86,7 +123,7 @@ def main() -> int:
 
     t = time.perf_counter()
     first = prefill()
-    log(f"  prefill (incl. upload) {time.perf_counter() - t:.1f}s")
+    log(f"  prefill (incl. weight upload) {time.perf_counter() - t:.1f}s")
     if args.warmup:
         model.decode_greedy(first, P, args.warmup)
     first = prefill()
@@ -96,17 +133,21 @@ def main() -> int:
     tok_s = args.steps / dt
     log(f"timed {args.steps} steps: {dt * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
 
-    # Dominant kernel, timed with HIP events on the stream it runs on.
-    us, kbytes = model.bench_kernel("gateup", 256)
-    k_gbs = kbytes / (us * 1e-6) / 1e9
-    per_kernel = {}
-    for kind in ("qkv", "oproj", "gateup", "down", "output"):
-        kus, kb = model.bench_kernel(kind, 64)
-        per_kernel[kind] = {"us": round(kus, 2), "GB/s": round(kb / (kus * 1e-6) / 1e9, 1),
-                            "bytes": int(kb)}
-    log(f"per-kernel: {per_kernel}")
+    # The decode step is one kernel launch: time it with HIP events on its
+    # stream at the middle position of the timed run (K/V rows up to there
+    # were written by the run above).
+    mid = P + args.steps // 2
+    us, sbytes = model.bench_token(int(toks[args.steps // 2 - 1]), mid, 32)
+    k_gbs = sbytes / (us * 1e-6) / 1e9
+    log(f"decode step at pos {mid}: {us:.1f} us, {sbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
+    copy_bytes = 1 << 30
+    cus = model.bench_copy(copy_bytes, 10)
+    copy_gbs = 2 * copy_bytes / (cus * 1e-6) / 1e9
+    log(f"device copy of 1 GiB: {cus:.1f} us -> {copy_gbs:.0f} GB/s (read + write)")
+    phases = phase_breakdown(model.phase_timeline(int(toks[args.steps // 2 - 1]), mid), spec.n_layer)
+    log(f"phase us per layer: {phases}")
 
-    # Whole-step floor: all weights once + KV read (mean seq) + KV write.
+    # Whole-run floor: all weights once + KV read (mean seq) + KV write.
     wbytes = configs.bytes_per_token_weights(spec)
     kvpos = configs.kv_bytes_per_position(spec)
     mean_seq = P + (args.steps + 1) / 2.0
@@ -114,30 +155,35 @@ def main() -> int:
     tok_gbs = tok_bytes * tok_s / 1e9
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and args.cpu_tokens > 0:
         from oracle import oracle as O
-        log(f"CPU baseline: oracle with {nthreads} threads, {P}-token prompt + {args.cpu_tokens} decode tokens")
+        n_fw = args.cpu_prompt + args.cpu_tokens
+        log(f"CPU baseline: oracle with {nthreads} threads, {args.cpu_prompt}-token prompt + "
+            f"{args.cpu_tokens} greedy tokens ({n_fw} forwards)")
         ref = O.OracleModel(model.gguf_view(), nthreads=nthreads)
-        tok = None
-        for p, t_ in enumerate(prompt):
+        c0 = time.perf_counter()
+        for p, t_ in enumerate(prompt[: args.cpu_prompt]):
             lg = ref.forward(t_, p)
         tok = O.argmax(lg)
         cpu_toks = []
-        c0 = time.perf_counter()
         for i in range(args.cpu_tokens):
             cpu_toks.append(tok)
-            lg = ref.forward(tok, P + i)
+            lg = ref.forward(tok, args.cpu_prompt + i)
             tok = O.argmax(lg)
         cdt = time.perf_counter() - c0
-        gpu_seq = [int(first)] + [int(x) for x in toks[: args.cpu_tokens - 1]]
-        match = cpu_toks == gpu_seq
-        log(f"  cpu {args.cpu_tokens / cdt:.2f} tok/s; greedy tokens match GPU: {match}")
         ref.close()
-        cpu = {"value": round(args.cpu_tokens / cdt, 3), "unit": "tok/s", "cores": nthreads,
-               "kind": "port",
-               "sample": f"C restatement of the reference CPU forward (oracle/talos_oracle.c), "
-                         f"same model and {P}-token prompt, {args.cpu_tokens} greedy decode tokens "
-                         f"(prefill untimed); greedy tokens identical to the GPU run: {match}"}
+        # the same short sequence on the GPU
+        model.reset()
+        for p, t_ in enumerate(prompt[: args.cpu_prompt]):
+            _, am = model.forward_token(t_, p, want_logits=False)
+        gpu_toks = [int(am)] + [int(x) for x in model.decode_greedy(am, args.cpu_prompt, args.cpu_tokens - 1)]
+        match = cpu_toks == gpu_toks
+        log(f"  cpu {n_fw / cdt:.3f} tok/s over {cdt:.1f}s; greedy tokens match GPU: {match}")
+        cpu = {"value": round(n_fw / cdt, 4), "unit": "tok/s", "cores": nthreads, "kind": "port",
+               "sample": f"oracle/talos_oracle.c (C restatement of the reference CPU forward, "
+                         f"{nthreads} OpenMP threads) on the same model: {args.cpu_prompt}-token prompt + "
+                         f"{args.cpu_tokens} greedy tokens = {n_fw} forwards, all timed; greedy tokens "
+                         f"identical to the GPU on the same sequence: {match}"}
 
     out = {
         "metric": METRIC,
@@ -156,14 +202,16 @@ def main() -> int:
                                "FFN 14336, vocab 32000, RoPE 1e6, Q4_0 matrices + Q6_K output, "
                                "random 32-token prompt then greedy decode, KV ctx 4096",
                    "batch": 1, "prompt_tokens": P, "weights": "Q4_0/Q6_K", "kv": "f32"},
-        "roofline": {"bound": "hbm", "kernel": "k_gateup (rmsnorm + gate/up Q4_0 matvec + SwiGLU)",
+        "roofline": {"bound": "hbm", "kernel": "k_mega (persistent decode step: 32 layers + output + argmax)",
                      "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": int(kbytes), "us_per_launch": round(us, 3)},
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": f"rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE ({TRAFFIC_FILE})",
+                     "bytes_per_launch": int(sbytes), "us_per_launch": round(us, 2), "pos": mid,
+                     "copy_kernel_GBs": round(copy_gbs, 1)},
         "token_roofline": {"bytes_per_token": int(tok_bytes), "achieved": round(tok_gbs, 1),
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
                            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1)},
-        "per_kernel": per_kernel,
+        "phase_us_per_layer": phases,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

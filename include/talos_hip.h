@@ -144,9 +144,24 @@ int talos_hip_matvec_dev(talos_hip_ctx* ctx, const char* name, const float* d_x,
 int talos_hip_bench_kernel(talos_hip_ctx* ctx, const char* kind, uint32_t reps, float* avg_us,
                            double* bytes);
 
+/* Time `reps` device-token steps (as talos_hip_forward_token, without the
+ * read-back) of `token` at `pos` with HIP events on the context's stream;
+ * returns the mean step time and the step's algorithmic bytes: all weights
+ * once (one embedding row), K/V rows 0..pos read, the K/V row at pos
+ * written, the logits.  Rewrites the K/V row at pos.  No reference
+ * counterpart: the roofline measurement of the decode step. */
+int talos_hip_bench_token(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint32_t reps, float* avg_us,
+                          double* bytes);
+
+/* Time `reps` launches of a plain device copy of nbytes (a multiple of 16):
+ * the HBM reference point, and the known-size kernel that scales the
+ * FETCH_SIZE / WRITE_SIZE counters.  No reference counterpart. */
+int talos_hip_bench_copy(talos_hip_ctx* ctx, size_t nbytes, uint32_t reps, float* avg_us);
+
 /* Profiling aid for the persistent decode kernel: run one device-token step
  * (as talos_hip_forward_token) and record, per workgroup, a wall-clock mark
- * at each phase boundary (11 per layer, then the head).  Writes nblocks *
+ * at each phase boundary (16 per layer: ten phase ends, a spare, five inside
+ * the first attention item; then the head).  Writes nblocks *
  * slots marks (cap must allow them) and the tick length in ns.  No reference
  * counterpart. */
 int talos_hip_phase_timeline(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint64_t* marks, size_t cap,

@@ -68,6 +68,8 @@ _SIGS = {
     "talos_hip_matvec": (C.c_int, [_P, C.c_char_p, _P, C.c_size_t, C.c_uint32, C.c_size_t, C.c_size_t, _F, _F]),
     "talos_hip_matvec_dev": (C.c_int, [_P, C.c_char_p, _P, _P]),
     "talos_hip_bench_kernel": (C.c_int, [_P, C.c_char_p, C.c_uint32, _F, C.POINTER(C.c_double)]),
+    "talos_hip_bench_token": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, _F, C.POINTER(C.c_double)]),
+    "talos_hip_bench_copy": (C.c_int, [_P, C.c_size_t, C.c_uint32, _F]),
     "talos_hip_phase_timeline": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64), C.c_size_t,
                                             _U32, _U32, C.POINTER(C.c_double)]),
     "talos_hip_stream": (_P, [_P]),
@@ -398,6 +400,26 @@ class Model:
         if rc:
             raise TalosError(rc, lib().talos_hip_last_error(h).decode())
         return us.value, b.value
+
+    def bench_token(self, token: int, pos: int, reps: int):
+        """(mean step microseconds, algorithmic bytes per step) of the
+        device-token decode step at `pos`, timed with HIP events."""
+        h = self.backend_handle()
+        us = C.c_float()
+        b = C.c_double()
+        rc = lib().talos_hip_bench_token(h, token, pos, reps, C.byref(us), C.byref(b))
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
+        return us.value, b.value
+
+    def bench_copy(self, nbytes: int, reps: int) -> float:
+        """Mean microseconds of a plain device copy of nbytes."""
+        h = self.backend_handle()
+        us = C.c_float()
+        rc = lib().talos_hip_bench_copy(h, nbytes, reps, C.byref(us))
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
+        return us.value
 
     def phase_timeline(self, token: int, pos: int):
         """Per-workgroup wall-clock marks (ns) of one persistent-kernel step:

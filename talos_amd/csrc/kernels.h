@@ -491,6 +491,20 @@ __global__ __launch_bounds__(256) void k_embed(DevMat M, const int32_t* state, f
   for (uint32_t e = threadIdx.x; e < M.cols; e += 256) x[e] = dq_elem(M, tok, e);
 }
 
+// ------------------------------------------------------- k_copy, k_fill --
+// Plain device copy (reference point for HBM bandwidth and for scaling the
+// FETCH_SIZE / WRITE_SIZE counters), and a fill of distinct values.
+__global__ __launch_bounds__(256) void k_copy(const u4* __restrict__ src, u4* __restrict__ dst, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+__global__ __launch_bounds__(256) void k_fill(u4* __restrict__ dst, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) {
+    const uint32_t v = (uint32_t)i * 2654435761u;
+    dst[i] = u4{v, v + 1, v + 2, v + 3};
+  }
+}
+
 // --------------------------------------------------------------- k_norm --
 // hidden = rmsnorm(x, output_norm) (src/model/llama.rs:180-181).
 __global__ __launch_bounds__(256) void k_norm(const float* x, const float* w, float eps, uint32_t n, float* out) {

@@ -87,6 +87,11 @@ struct talos_hip_ctx {
   float* mact = nullptr;   // per-layer activation slots
   float* mpart = nullptr;  // per-layer attention slice partials
   bool mega_prefetch = true;  // TALOS_HIP_PREFETCH=0 turns cross-barrier weight prefetch off
+  // TALOS_HIP_COOP=0 launches the persistent kernel with an ordinary launch
+  // (same grid, one workgroup per CU), for tools that mishandle cooperative
+  // launches.  Co-residency is then not promised by the runtime; a barrier
+  // that cannot complete times out and the step reports an error.
+  bool mega_coop = true;
   MegaParams mp{};
 };
 
@@ -643,8 +648,12 @@ int mega_launch(talos_hip_ctx* c, GraphKind kind, uint64_t* timeline = nullptr) 
   P.hidden_only = kind == G_HIDDEN;
   P.argmax = kind == G_GREEDY ? 2 : (kind == G_TOKEN ? 1 : 0);
   void* args[] = {&P};
-  HIPCHK(c, hipLaunchCooperativeKernel(c->mega_fn, dim3(c->mega_blocks), dim3(MEGA_NT), args,
-                                       (unsigned)c->mega_lds, c->stream));
+  if (c->mega_coop)
+    HIPCHK(c, hipLaunchCooperativeKernel(c->mega_fn, dim3(c->mega_blocks), dim3(MEGA_NT), args,
+                                         (unsigned)c->mega_lds, c->stream));
+  else
+    HIPCHK(c, hipLaunchKernel(c->mega_fn, dim3(c->mega_blocks), dim3(MEGA_NT), args, (unsigned)c->mega_lds,
+                              c->stream));
   return TALOS_OK;
 }
 
@@ -707,6 +716,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_mega = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_PREFETCH");
   c->mega_prefetch = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_COOP");
+  c->mega_coop = !(env && env[0] == '0');
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;
@@ -1035,6 +1046,90 @@ int talos_hip_bench_kernel(talos_hip_ctx* c, const char* kind, uint32_t reps, fl
   (void)hipEventDestroy(e1);
   *avg_us = ms * 1000.f / (float)reps;
   *bytes = b;
+  return TALOS_OK;
+}
+
+int talos_hip_bench_token(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint32_t reps, float* avg_us,
+                          double* bytes) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!avg_us || !bytes || !reps) return fail(c, TALOS_ERR_ARG, "bad argument");
+  const auto& cf = c->cfg;
+  if (pos >= cf.context_length) return fail(c, TALOS_ERR_POS, "pos %u >= context_length %u", pos, cf.context_length);
+  if (token >= cf.vocab_size) return fail(c, TALOS_ERR_TOKEN, "token %u >= vocab_size %u", token, cf.vocab_size);
+  if ((rc = set_device(c))) return rc;
+  // Algorithmic bytes of one step: every weight once (the embedding row
+  // only), the K/V rows 0..pos read, the K/V row at pos written, the logits.
+  double b = 0;
+  for (uint32_t l = 0; l < cf.n_layer; ++l) {
+    LayerW w;
+    if ((rc = layer_weights(c, l, &w))) return rc;
+    b += (double)(w.q->len + w.k->len + w.v->len + w.o->len + w.g->len + w.u->len + w.d->len) + 8.0 * cf.n_embd;
+  }
+  const DevWeight *wout, *emb;
+  const float* onorm;
+  if ((rc = need_matrix(c, "output.weight", cf.vocab_size, cf.n_embd, &wout)) ||
+      (rc = need_norm(c, "output_norm.weight", cf.n_embd, &onorm)) ||
+      (rc = need_matrix(c, "token_embd.weight", cf.vocab_size, cf.n_embd, &emb)))
+    return rc;
+  const double kv_row = 2.0 * 4.0 * c->kv_dim;  // K and V, f32
+  b += (double)wout->len + 4.0 * cf.n_embd + (double)emb->len / cf.vocab_size;
+  b += (double)cf.n_layer * kv_row * ((double)pos + 2.0) + 4.0 * cf.vocab_size;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_TOKEN, &g))) return rc;
+  if ((rc = set_state(c, token, pos))) return rc;
+  if ((rc = run_step(c, G_TOKEN, g))) return rc;  // warm
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (uint32_t r = 0; r < reps && rc == TALOS_OK; ++r) rc = run_step(c, G_TOKEN, g);
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float ms = 0;
+  HIPCHK(c, hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  HIPCHK(c, hipMemcpy(c->h_io, c->io, 64, hipMemcpyDeviceToHost));
+  if ((rc = check_device_err(c))) return rc;
+  *avg_us = ms * 1000.f / (float)reps;
+  *bytes = b;
+  return TALOS_OK;
+}
+
+int talos_hip_bench_copy(talos_hip_ctx* c, size_t nbytes, uint32_t reps, float* avg_us) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!avg_us || !reps || nbytes < 16 || nbytes % 16) return fail(c, TALOS_ERR_ARG, "bad argument");
+  if ((rc = set_device(c))) return rc;
+  void *src = nullptr, *dst = nullptr;
+  HIPCHK(c, hipMalloc(&src, nbytes));
+  if (hipMalloc(&dst, nbytes) != hipSuccess) {
+    (void)hipFree(src);
+    return fail(c, TALOS_ERR_HIP, "hipMalloc of %zu bytes failed", nbytes);
+  }
+  const size_t n16 = nbytes / 16;
+  hipDeviceProp_t prop;
+  HIPCHK(c, hipGetDeviceProperties(&prop, c->cfg.device));
+  const uint32_t grid = (uint32_t)prop.multiProcessorCount * 8;
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  k_fill<<<grid, 256, 0, c->stream>>>(reinterpret_cast<u4*>(src), n16);
+  k_copy<<<grid, 256, 0, c->stream>>>(reinterpret_cast<const u4*>(src), reinterpret_cast<u4*>(dst), n16);
+  HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (uint32_t r = 0; r < reps; ++r)
+    k_copy<<<grid, 256, 0, c->stream>>>(reinterpret_cast<const u4*>(src), reinterpret_cast<u4*>(dst), n16);
+  HIPCHK(c, hipEventRecord(e1, c->stream));
+  HIPCHK(c, hipEventSynchronize(e1));
+  float ms = 0;
+  HIPCHK(c, hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipFree(src);
+  (void)hipFree(dst);
+  *avg_us = ms * 1000.f / (float)reps;
   return TALOS_OK;
 }
 
