@@ -68,6 +68,19 @@ def lib() -> C.CDLL:
             "tor_model_reset": (None, [C.c_void_p]),
             "tor_model_kv_len": (C.c_size_t, [C.c_void_p]),
             "tor_model_set_kv": (C.c_int, [C.c_void_p, _F, _F, C.c_size_t]),
+            "tor_gguf_parse": (C.c_void_p, [C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
+            "tor_gguf_free": (None, [C.c_void_p]),
+            "tor_gguf_get_u32": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32)]),
+            "tor_gguf_get_f32": (C.c_int, [C.c_void_p, C.c_char_p, _F]),
+            "tor_gguf_get_str": (C.c_char_p, [C.c_void_p, C.c_char_p]),
+            "tor_gguf_arr_str_len": (C.c_long, [C.c_void_p, C.c_char_p]),
+            "tor_gguf_tensor_count": (C.c_size_t, [C.c_void_p]),
+            "tor_gguf_tensor_info": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_char_p),
+                                               C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                               C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
+            "tor_gguf_tensor_raw": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p),
+                                              C.POINTER(C.c_size_t), C.POINTER(C.c_int), C.c_char_p,
+                                              C.c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -228,3 +241,58 @@ class OracleModel:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         lib().tor_model_set_kv(self._h, _f(k), _f(v), k.shape[1])
+
+
+class OracleGguf:
+    """GGUF v3 parse (src/gguf/reader.rs:193-351) over bytes kept alive here."""
+
+    def __init__(self, data: bytes):
+        self._keep = np.frombuffer(bytes(data), np.uint8).copy()
+        err = C.create_string_buffer(512)
+        h = lib().tor_gguf_parse(C.c_void_p(self._keep.ctypes.data), self._keep.size, err, 512)
+        if not h:
+            raise ValueError(err.value.decode())
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().tor_gguf_free(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def u32(self, key: str):
+        v = C.c_uint32()
+        return v.value if lib().tor_gguf_get_u32(self._h, key.encode(), C.byref(v)) else None
+
+    def f32(self, key: str):
+        v = C.c_float()
+        return v.value if lib().tor_gguf_get_f32(self._h, key.encode(), C.byref(v)) else None
+
+    def str(self, key: str):
+        v = lib().tor_gguf_get_str(self._h, key.encode())
+        return v.decode() if v is not None else None
+
+    def arr_str_len(self, key: str) -> int:
+        return lib().tor_gguf_arr_str_len(self._h, key.encode())
+
+    def tensors(self):
+        out = []
+        for i in range(lib().tor_gguf_tensor_count(self._h)):
+            name = C.c_char_p()
+            nd = C.c_uint32()
+            dims = (C.c_uint64 * 4)()
+            ty = C.c_uint32()
+            off = C.c_uint64()
+            lib().tor_gguf_tensor_info(self._h, i, C.byref(name), C.byref(nd), dims, C.byref(ty), C.byref(off))
+            out.append((name.value.decode(), [dims[k] for k in range(nd.value)], ty.value, off.value))
+        return out
+
+    def tensor_raw(self, name: str):
+        p = C.c_void_p()
+        n = C.c_size_t()
+        ty = C.c_int()
+        err = C.create_string_buffer(256)
+        if lib().tor_gguf_tensor_raw(self._h, name.encode(), C.byref(p), C.byref(n), C.byref(ty), err, 256):
+            raise KeyError(err.value.decode())
+        return ty.value, bytes((C.c_uint8 * n.value).from_address(p.value))
