@@ -82,6 +82,28 @@ def phase_breakdown(tl, n_layer: int, per_layer: int = 16) -> dict:
     return {k: round(float(np.mean(v)) / 1e3, 2) for k, v in seg.items() if v}
 
 
+def matvec_microbench(T) -> dict:
+    """W[4096 x 4096] . x[4096] in F32, Q8_0 and Q4_0 (W ~ N(0, 0.02)),
+    rotating over enough resident copies (> 256 MB) that every launch
+    streams W from HBM.  GB/s of algorithmic bytes (W + x + y)."""
+    n = 4096
+    be = T.HipBackend(1, 32, 8, n, n, 32, 16)
+    w = T.synth_normal(7, "matvec.W", 0, n * n, 0.02)
+    res = {}
+    for name, t, data in (("F32", T.GGML_F32, w), ("Q8_0", T.GGML_Q8_0, T.quantize(T.GGML_Q8_0, w)),
+                          ("Q4_0", T.GGML_Q4_0, T.quantize(T.GGML_Q4_0, w))):
+        copies = max(2, (512 << 20) // data.nbytes + 1)
+        names = [f"mv.{name}.{i}" for i in range(copies)]
+        for nm in names:
+            be.upload(nm, data, t, n, n)
+        us, b = be.bench_matvec(names, 256)
+        res[name] = {"us": round(us, 2), "GB/s": round(b / (us * 1e-6) / 1e9, 1),
+                     "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b)}
+    be.close()
+    log(f"matvec 4096x4096: {res}")
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +168,20 @@ def main() -> int:
     log(f"device copy of 1 GiB: {cus:.1f} us -> {copy_gbs:.0f} GB/s (read + write)")
     phases = phase_breakdown(model.phase_timeline(int(toks[args.steps // 2 - 1]), mid), spec.n_layer)
     log(f"phase us per layer: {phases}")
+
+    # The host-buffer boundary (talos_hip_forward: embedding row in, logits
+    # out over PCIe), for comparison with the device-resident token loop.
+    model.reset()
+    for p, tok in enumerate(prompt):
+        model.forward_token(tok, p, want_logits=False)
+    t1 = time.perf_counter()
+    npc = 32
+    for i in range(npc):
+        lg = model.forward_gpu(int(toks[i]), P + i)
+    pcie_tok_s = npc / (time.perf_counter() - t1)
+    log(f"host-boundary forward (x_embed H2D + logits D2H): {pcie_tok_s:.1f} tok/s")
+
+    matvec = matvec_microbench(T)
 
     # Whole-run floor: all weights once + KV read (mean seq) + KV write.
     wbytes = configs.bytes_per_token_weights(spec)
@@ -212,6 +248,8 @@ def main() -> int:
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
                            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1)},
         "phase_us_per_layer": phases,
+        "host_boundary_tok_s": round(pcie_tok_s, 2),
+        "matvec_4096x4096": matvec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -135,6 +135,15 @@ int talos_hip_matvec(talos_hip_ctx* ctx, const char* name, const void* bytes, si
  * the context's stream and not waited for. */
 int talos_hip_matvec_dev(talos_hip_ctx* ctx, const char* name, const float* d_x, float* d_out);
 
+/* Time `reps` standalone matvecs (as talos_hip_matvec_dev) rotating over the
+ * resident weights `names` (one shape; give more bytes than the 256 MB MALL
+ * so every launch streams from HBM), with HIP events on the context's
+ * stream.  Writes the mean launch duration (us) and the algorithmic bytes of
+ * one launch (the weight bytes plus x and y).  No reference counterpart: the
+ * matvec microbenchmark (metal/mod.rs:195-253 is the API it times). */
+int talos_hip_bench_matvec(talos_hip_ctx* ctx, const char* const* names, uint32_t n_names, uint32_t reps,
+                           float* avg_us, double* bytes);
+
 /* Time one decode kernel kind ("qkv", "oproj", "gateup", "down", "output")
  * with HIP events on the context's stream: `reps` back-to-back launches on
  * the resident weights, rotating through the layers so the weights stream

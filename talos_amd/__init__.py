@@ -69,6 +69,8 @@ _SIGS = {
     "talos_hip_matvec_dev": (C.c_int, [_P, C.c_char_p, _P, _P]),
     "talos_hip_bench_kernel": (C.c_int, [_P, C.c_char_p, C.c_uint32, _F, C.POINTER(C.c_double)]),
     "talos_hip_bench_token": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, _F, C.POINTER(C.c_double)]),
+    "talos_hip_bench_matvec": (C.c_int, [_P, C.POINTER(C.c_char_p), C.c_uint32, C.c_uint32, _F,
+                                         C.POINTER(C.c_double)]),
     "talos_hip_bench_copy": (C.c_int, [_P, C.c_size_t, C.c_uint32, _F]),
     "talos_hip_phase_timeline": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64), C.c_size_t,
                                             _U32, _U32, C.POINTER(C.c_double)]),
@@ -210,6 +212,15 @@ class HipBackend:
         us = C.c_float()
         b = C.c_double()
         self._check(lib().talos_hip_bench_kernel(self._h, kind.encode(), reps, C.byref(us), C.byref(b)))
+        return us.value, b.value
+
+    def bench_matvec(self, names, reps: int):
+        """(mean launch microseconds, algorithmic bytes per launch) of the
+        standalone matvec rotating over the resident weights `names`."""
+        arr = (C.c_char_p * len(names))(*[n.encode() for n in names])
+        us = C.c_float()
+        b = C.c_double()
+        self._check(lib().talos_hip_bench_matvec(self._h, arr, len(names), reps, C.byref(us), C.byref(b)))
         return us.value, b.value
 
     def stream(self) -> int:

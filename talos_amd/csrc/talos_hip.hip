@@ -997,6 +997,50 @@ int talos_hip_matvec_dev(talos_hip_ctx* c, const char* name, const float* d_x, f
   return enqueue_matvec(c, w, d_x, d_out);
 }
 
+int talos_hip_bench_matvec(talos_hip_ctx* c, const char* const* names, uint32_t n_names, uint32_t reps,
+                           float* avg_us, double* bytes) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!names || !n_names || !reps || !avg_us || !bytes) return fail(c, TALOS_ERR_ARG, "bad argument");
+  if ((rc = set_device(c))) return rc;
+  std::vector<const DevWeight*> ws(n_names);
+  for (uint32_t i = 0; i < n_names; ++i) {
+    ws[i] = names[i] ? find_w(c, names[i]) : nullptr;
+    if (!ws[i]) return fail(c, TALOS_ERR_MISSING_WEIGHT, "weight \"%s\" is not resident", names[i] ? names[i] : "");
+    if (ws[i]->rows != ws[0]->rows || ws[i]->cols != ws[0]->cols)
+      return fail(c, TALOS_ERR_SHAPE, "bench matrices must share one shape");
+  }
+  const size_t rows = ws[0]->rows, cols = ws[0]->cols;
+  float *x = nullptr, *out = nullptr;
+  HIPCHK(c, hipMalloc(&x, cols * 4));
+  if (hipMalloc(&out, rows * 4) != hipSuccess) {
+    (void)hipFree(x);
+    return fail(c, TALOS_ERR_HIP, "hipMalloc failed");
+  }
+  HIPCHK(c, hipMemsetAsync(x, 0, cols * 4, c->stream));
+  hipEvent_t e0, e1;
+  HIPCHK(c, hipEventCreate(&e0));
+  HIPCHK(c, hipEventCreate(&e1));
+  rc = enqueue_matvec(c, ws[0], x, out);  // warm
+  if (!rc) HIPCHK(c, hipEventRecord(e0, c->stream));
+  for (uint32_t r = 0; r < reps && !rc; ++r) rc = enqueue_matvec(c, ws[(r + 1) % n_names], x, out);
+  if (!rc) {
+    HIPCHK(c, hipEventRecord(e1, c->stream));
+    HIPCHK(c, hipEventSynchronize(e1));
+  }
+  float ms = 0;
+  if (!rc) HIPCHK(c, hipEventElapsedTime(&ms, e0, e1));
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  (void)hipFree(x);
+  (void)hipFree(out);
+  if (rc) return rc;
+  *avg_us = ms * 1000.f / (float)reps;
+  *bytes = (double)ws[0]->len + 4.0 * (double)(rows + cols);
+  return TALOS_OK;
+}
+
 int talos_hip_bench_kernel(talos_hip_ctx* c, const char* kind, uint32_t reps, float* avg_us, double* bytes) {
   int rc;
   if ((rc = check_ctx(c))) return rc;
