@@ -11,6 +11,16 @@
  * fp32 with no contraction (built with -ffp-contract=off), transcendental
  * calls go to glibc powf/sinf/cosf/expf/sqrtf as Rust's f32 methods do on
  * Linux.
+ *
+ * Pinning (tests/test_oracle_kat.py, tests/test_oracle_model.py): every
+ * function is checked against the reference's own unit-test values, closed
+ * forms, layout probes or brute force, and the composed forward against the
+ * GQA == replicated-MHA invariant and an independent float64 forward.
+ * Parity unpinned: bit-for-bit equality with the Rust CPU path.  tor_dot
+ * takes matmul::dot's wide::f32x8 mul_add as unfused and its reduce_add as a
+ * left-to-right sum of the 8 lanes; the `wide` crate is not available to
+ * confirm either, so results agree with the reference to fp32 reordering
+ * error, not to the bit.
  */
 #ifndef TALOS_ORACLE_H
 #define TALOS_ORACLE_H

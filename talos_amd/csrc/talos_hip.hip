@@ -5,9 +5,13 @@
 //  * weights are repacked once at upload (layout.h) and stay resident in HBM,
 //    keyed by tensor name;
 //  * the K/V cache, residual stream and activations stay on the device;
-//  * a token step is ~5 kernels per layer (kernels.h) captured once into a
-//    hipGraph whose position/token come from device memory, so every step is
-//    one graph launch plus the logits read-back.
+//  * a token step is one launch of the persistent kernel (mega.h: every
+//    layer, the output projection and the argmax, phases separated by grid
+//    barriers) reading position/token from device memory;
+//  * models without a persistent-kernel instantiation (mixed layer formats,
+//    shapes it does not take) run ~5 kernels per layer (kernels.h) captured
+//    once into a hipGraph.  Either way only the logits (or nothing, in the
+//    device token loop) are read back.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
