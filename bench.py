@@ -31,8 +31,8 @@ if ROOT not in sys.path:
 
 METRIC = "decode tok/s batch-1 @7B-shape Q4_0; matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
-PHASES = ["qkv_work", "attn_barrier", "attn_work", "o_barrier_stage", "o_work", "gateup_barrier_stage",
-          "gateup_work", "down_barrier_stage", "down_work", "next_layer_barrier_stage"]
+PHASES = ["qkv_work", "attn_barrier", "attn_work", "o_barrier", "o_stage", "o_work", "gateup_barrier",
+          "gateup_stage", "gateup_work", "down_barrier", "down_stage", "down_work", "next_barrier", "next_stage"]
 
 
 def host_threads() -> int:
@@ -66,19 +66,27 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def phase_breakdown(tl, n_layer: int, per_layer: int = 16) -> dict:
+def phase_breakdown(tl, n_layer: int, per_layer: int = 20, bar: int = 16) -> dict:
     """Mean microseconds per layer of each phase of one step, from the
-    latest workgroup's mark at each phase boundary."""
+    latest workgroup's mark at each phase boundary (marks per layer: 0 qkv
+    staged, 1 qkv end, 2 attention barrier passed, 3 attention end, 4 o
+    staged, 5 o end, 6 gate/up staged, 7 gate/up end, 8 down staged, 9 down
+    end; bar + 0..3: barrier passed before the qkv, o, gate/up and down
+    staging)."""
     import numpy as np
     mx = tl.max(axis=0)
     seg = {k: [] for k in PHASES}
     for l in range(n_layer):
         b = l * per_layer
-        d = [mx[b + i + 1] - mx[b + i] for i in range(9)]
-        for k, v in zip(PHASES[:9], d):
+        m = lambda i: mx[b + i]
+        vals = [m(1) - m(0), m(2) - m(1), m(3) - m(2), m(bar + 1) - m(3), m(4) - m(bar + 1), m(5) - m(4),
+                m(bar + 2) - m(5), m(6) - m(bar + 2), m(7) - m(6), m(bar + 3) - m(7), m(8) - m(bar + 3),
+                m(9) - m(8)]
+        for k, v in zip(PHASES[:12], vals):
             seg[k].append(v)
         if l + 1 < n_layer:
-            seg[PHASES[9]].append(mx[b + per_layer] - mx[b + 9])
+            seg["next_barrier"].append(mx[b + per_layer + bar] - m(9))
+            seg["next_stage"].append(mx[b + per_layer] - mx[b + per_layer + bar])
     return {k: round(float(np.mean(v)) / 1e3, 2) for k, v in seg.items() if v}
 
 

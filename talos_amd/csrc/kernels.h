@@ -97,7 +97,8 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
     r0 = p * R;
     rmax = A0.rows;
   };
-  auto stage = [&] {
+  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
+    pf();
     stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
   };
   auto epi = [&](int k, const float(&y)[R]) {
@@ -110,10 +111,10 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
     for (int r = 0; r < R; r += 2) {
       const uint32_t row = r0 + r;
       const float y0 = y[r], y1 = y[r + 1];
+      const uint32_t i = (row % P.hd) / 2;  // loaded for v rows too (exact wait counts)
+      const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
+      const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
       if (s < 2) {
-        const uint32_t i = (row % P.hd) / 2;
-        const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
-        const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
         const float a = y0 * c - y1 * sn;
         const float b = y0 * sn + y1 * c;
         float* dst = s == 0 ? P.q_out + row : P.kc + (size_t)pos * P.kv_dim + row;
@@ -159,7 +160,8 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
     r0 = (ubase + k) * R;
     rmax = P.m.rows;
   };
-  auto stage = [&] {
+  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
+    pf();
     stage_x(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
             P.need & 2);
   };
@@ -207,7 +209,8 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
     r0 = (ubase + k) * PR;
     rmax = P.g.rows;
   };
-  auto stage = [&] {
+  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
+    pf();
     stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
   };
   auto epi = [&](int k, const float(&y)[R]) {

@@ -40,17 +40,25 @@ __device__ __forceinline__ u4 ldg4(const uint8_t* p) {
 // ---- per-format block dots: the dot of one block's raw (unsigned) quants
 // with x, minus the quant offset folded in through the x group sums.
 
+// A masked word whose known-zero bits the compiler may not exploit: with
+// them visible it folds mask + byte extract into v_bfe_u32 + cvt_f32_ubyte0
+// (two ops per element) instead of one v_cvt_f32_ubyte{0..3} per element.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ float q4_block_dot(u4 q, const f4* x, float xs8) {
   float s = 0.f;
-  s = dot_ub4(q.x & 0x0F0F0F0Fu, x[0], s);
-  s = dot_ub4(q.y & 0x0F0F0F0Fu, x[1], s);
-  s = dot_ub4(q.z & 0x0F0F0F0Fu, x[2], s);
-  s = dot_ub4(q.w & 0x0F0F0F0Fu, x[3], s);
+  s = dot_ub4(opaque(q.x & 0x0F0F0F0Fu), x[0], s);
+  s = dot_ub4(opaque(q.y & 0x0F0F0F0Fu), x[1], s);
+  s = dot_ub4(opaque(q.z & 0x0F0F0F0Fu), x[2], s);
+  s = dot_ub4(opaque(q.w & 0x0F0F0F0Fu), x[3], s);
   float t = 0.f;
-  t = dot_ub4((q.x >> 4) & 0x0F0F0F0Fu, x[4], t);
-  t = dot_ub4((q.y >> 4) & 0x0F0F0F0Fu, x[5], t);
-  t = dot_ub4((q.z >> 4) & 0x0F0F0F0Fu, x[6], t);
-  t = dot_ub4((q.w >> 4) & 0x0F0F0F0Fu, x[7], t);
+  t = dot_ub4(opaque((q.x >> 4) & 0x0F0F0F0Fu), x[4], t);
+  t = dot_ub4(opaque((q.y >> 4) & 0x0F0F0F0Fu), x[5], t);
+  t = dot_ub4(opaque((q.z >> 4) & 0x0F0F0F0Fu), x[6], t);
+  t = dot_ub4(opaque((q.w >> 4) & 0x0F0F0F0Fu), x[7], t);
   return (s + t) - xs8;
 }
 
@@ -81,10 +89,10 @@ __device__ __forceinline__ float q6_chunk_dot(u4 a, u4 b, u4 h, uint32_t scw, co
     const uint32_t q2 = (bv[k] & 0x0F0F0F0Fu) | ((hv[k] & 0x0C0C0C0Cu) << 2);
     const uint32_t q3 = ((av[k] >> 4) & 0x0F0F0F0Fu) | (hv[k] & 0x30303030u);
     const uint32_t q4 = ((bv[k] >> 4) & 0x0F0F0F0Fu) | ((hv[k] & 0xC0C0C0C0u) >> 2);
-    r0 = dot_ub4(q1, x[k], r0);
-    r1 = dot_ub4(q2, x[4 + k], r1);
-    r2 = dot_ub4(q3, x[8 + k], r2);
-    r3 = dot_ub4(q4, x[12 + k], r3);
+    r0 = dot_ub4(opaque(q1), x[k], r0);
+    r1 = dot_ub4(opaque(q2), x[4 + k], r1);
+    r2 = dot_ub4(opaque(q3), x[8 + k], r2);
+    r3 = dot_ub4(opaque(q4), x[12 + k], r3);
   }
   const float s0 = (float)(int8_t)(scw & 0xFF), s1 = (float)(int8_t)((scw >> 8) & 0xFF);
   const float s2 = (float)(int8_t)((scw >> 16) & 0xFF), s3 = (float)(int8_t)(scw >> 24);

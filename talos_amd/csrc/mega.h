@@ -13,6 +13,7 @@
 #pragma once
 #include "coherent.h"
 #include "kernels.h"
+#include "mfma.h"
 
 #define MEGA_NT 512
 #define MEGA_NW (MEGA_NT / 64)
@@ -89,12 +90,14 @@ __device__ __forceinline__ float* mega_base(const MegaParams& P, uint32_t l) {
   return (l == 0 && !P.embed) ? P.x : mega_act(P, l, MEGA_ACT_BASE);
 }
 
-// Phase timeline: per layer 16 marks (qkv staged/end, attention barrier/end,
-// o staged/end, gate-up staged/end, down staged/end, one spare, then five
-// inside the block's first attention item: inputs loaded, softmax done, PV
-// reduced, slice published, item done), then head.
-#define MEGA_TL_PER_LAYER 16
+// Phase timeline: per layer 20 marks (qkv staged/end, attention barrier/end,
+// o staged/end, gate-up staged/end, down staged/end, one spare, five inside
+// the block's first attention item: inputs loaded, softmax done, PV reduced,
+// slice published, item done; then the barrier-passed marks of the qkv, o,
+// gate-up and down phases), then head.
+#define MEGA_TL_PER_LAYER 20
 #define MEGA_TL_ATTN 11
+#define MEGA_TL_BAR 16
 #define MEGA_TL_SLOTS(n_layer) ((n_layer) * MEGA_TL_PER_LAYER + 8)
 #define MEGA_MARK(P, slot)                                                                   \
   do {                                                                                       \
@@ -105,16 +108,24 @@ __device__ __forceinline__ float* mega_base(const MegaParams& P, uint32_t l) {
 static inline size_t mega_sync_words(uint32_t nblocks) { return (size_t)nblocks * 16 + 64 + 2 * nblocks + 64; }
 
 // Stage n floats into the LDS layouts, optionally as rmsnorm(x)*w
-// (src/math/ops.rs:5-12), with every load of the block issued in one batch
-// (one memory round trip).  src(e) yields x[e..e+3] for e % 4 == 0; the
-// block also publishes the staged raw values of [pub_lo, pub_hi) to `pub`.
-// Requires n % 4 == 0 and n <= MEGA_STAGE_MAX.
+// (src/math/ops.rs:5-12), with every load of the block (x and the norm
+// weights) issued in one batch (one memory round trip).  `after()` runs
+// right after that batch is issued: loads it issues complete after the
+// staging loads (a wave's vector memory operations complete in order), so the
+// matvec's first weight loads go there.  src(e) yields x[e..e+3] for
+// e % 4 == 0; the block also publishes the staged raw values of
+// [pub_lo, pub_hi) to `pub`.  Requires n % 4 == 0 and n <= MEGA_STAGE_MAX.
+// VPT float4 per thread: the caller picks the smallest that covers n
+// (mega_stage below).
 #define MEGA_VPT 8
 #define MEGA_STAGE_MAX (MEGA_VPT * MEGA_NT * 4)
 
-template <class Src>
-__device__ __forceinline__ void mega_stage(Src src, int n, const float* __restrict__ w, float eps, bool norm,
-                                           const XStage& X, int need, float* pub, int pub_lo, int pub_hi) {
+template <int MEGA_VPT_N, class Src, class After>
+__device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __restrict__ w, float eps, bool norm,
+                                             const XStage& X, int need, float* pub, int pub_lo, int pub_hi,
+                                             After after) {
+#undef MEGA_VPT
+#define MEGA_VPT MEGA_VPT_N
   // Opaque copy of the thread index: keeps the compiler from hoisting this
   // index arithmetic out of the layer loop (which would keep it live, and
   // spilled, across every phase).
@@ -125,11 +136,22 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
   f4 v[MEGA_VPT];
   // Loads are unconditional (index clamped) so they issue as one batch;
   // out-of-range groups are zeroed afterwards.
+  f4 wv[MEGA_VPT];
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i) {
     const int e4 = i * MEGA_NT + tid;
     v[i] = src((e4 < nr ? e4 : nr - 1) * 4);
   }
+  if (norm) {
+#pragma unroll
+    for (int i = 0; i < MEGA_VPT; ++i) {
+      const int e4 = i * MEGA_NT + tid;
+      wv[i] = gld4(w + (e4 < nr ? e4 : nr - 1) * 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  after();
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i)
     if (i * MEGA_NT + tid >= nr) v[i] = f4{0.f, 0.f, 0.f, 0.f};
@@ -148,7 +170,7 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
     if (e4 < n4) {
       if (pub && e4 < nr && e4 * 4 >= pub_lo && e4 * 4 < pub_hi) st_coh4(pub + e4 * 4, x);
       if (norm && e4 < nr) {
-        const f4 ww = gld4(w + e4 * 4);
+        const f4 ww = wv[i];
         x.x = x.x * scale * ww.x;
         x.y = x.y * scale * ww.y;
         x.z = x.z * scale * ww.z;
@@ -162,6 +184,34 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
     if (e4 < n4 && (tid & 3) == 0) X.xsum[e4 >> 2] = s;
   }
   __syncthreads();
+#undef MEGA_VPT
+#define MEGA_VPT 8
+}
+
+template <class Src, class After>
+__device__ __forceinline__ void mega_stage(Src src, int n, const float* __restrict__ w, float eps, bool norm,
+                                           const XStage& X, int need, float* pub, int pub_lo, int pub_hi,
+                                           After after) {
+  if (n <= 2 * MEGA_NT * 4)
+    mega_stage_v<2>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after);
+  else
+    mega_stage_v<MEGA_VPT>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after);
+}
+
+// Groups per block the matrix-core phases may need (LDS partial sums).
+#define MEGA_GPB 8
+
+// stage_xq with the fewest rounds of 8 elements per thread covering n.
+template <class Src, class After>
+__device__ __forceinline__ void stage_xq_n(Src src, int n, const float* w, float eps, bool norm, const XQ& X,
+                                           float* pub, int pub_lo, int pub_hi, After after) {
+  const int n8 = n >> 3;
+  if (n8 <= MEGA_NT)
+    stage_xq<1, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
+  else if (n8 <= 2 * MEGA_NT)
+    stage_xq<2, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
+  else
+    stage_xq<4, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
 }
 
 // x[e..e+3] of one array, of a + b, or of (a + b) + c: the residual stream
@@ -438,7 +488,9 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
 #undef ATTN_MARK
 }
 
-template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL>
+// MF: the layer matvecs (Q4_0) run on the matrix cores (mfma.h); UN and UF
+// are then the tiles per wave of the n- and ff-wide rows (cols / 1024).
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, bool MF>
 __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -459,10 +511,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   constexpr int RL = mv_rows(LF), RO = mv_rows(OF);
   constexpr int LL = MvT<LF>::L, LO = MvT<OF>::L;
   const int need_l = 1 << LL, need_o = 1 << LO;
-  // block 0 gathers the barrier arrivals, so it issues no loads before waiting
-  const bool pre = P.prefetch && blockIdx.x != 0;
+  // each matvec phase issues its first weight loads right behind its staging
+  // loads
+  const bool pre = P.prefetch != 0;
   // this block's slice of the residual base it publishes each layer
-  const int slice = (((int)P.n + (int)nb - 1) / (int)nb + 3) & ~3;
+  const int slice = (((int)P.n + (int)nb - 1) / (int)nb + 7) & ~7;
   const int pub_lo = (int)blockIdx.x * slice, pub_hi = pub_lo + slice;
   auto arrive = [&] { grid_arrive(G, ep + 1); };
   auto wait = [&] { grid_wait(G, ++ep); };
@@ -480,7 +533,59 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     float* h = mega_act(P, l, MEGA_ACT_H);
     float* d_out = mega_act(P, l, MEGA_ACT_D);
     // ---- qkv: rmsnorm(x) -> q/k/v -> RoPE -> q, K/V row at pos
-    {
+    if constexpr (MF) {
+      const XQ X = carve_xq(smem, P.n, MEGA_GPB, MEGA_NW);
+      const int g_q = (int)P.n / 16, g_kv = (int)P.kv_dim / 16, ngr = g_q + 2 * g_kv;
+      const int gpb = (ngr + (int)nb - 1) / (int)nb;
+      auto seg = [&](int gi, int& s, uint32_t& row0) {
+        s = gi < g_q ? 0 : (gi < g_q + g_kv ? 1 : 2);
+        row0 = (uint32_t)(s == 0 ? gi : (s == 1 ? gi - g_q : gi - g_q - g_kv)) * 16;
+      };
+      auto grp = [&](int gi, DevMat& M0, DevMat& M1, uint32_t& row0) {
+        int s;
+        seg(gi, s, row0);
+        M0 = s == 0 ? const_mat(&LP->q) : (s == 1 ? const_mat(&LP->k) : const_mat(&LP->v));
+        M1 = M0;
+      };
+      auto arr = [&] {
+        if (l > 0) arrive();
+      };
+      auto stage = [&](auto&& pf) {
+        if (l > 0) {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
+          // x = (base + attproj) + down of the previous layer; publish it
+          Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf);
+        } else if (P.embed) {
+          EmbSrc src{P.embd, tok};
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf);
+        } else {
+          Src1 src{P.x};
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, nullptr, 0, 0, pf);
+        }
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
+      };
+      auto fin = [&](int gi, int jj, float y0, float y1) {
+        int s;
+        uint32_t row0;
+        seg(gi, s, row0);
+        const uint32_t row = row0 + 2 * jj;
+        const uint32_t i = (row % P.hd) / 2;
+        const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
+        const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
+        if (s < 2) {
+          float* dst = s == 0 ? q + row : LP->kc + (size_t)pos * P.kv_dim + row;
+          st_coh(dst, y0 * c - y1 * sn);
+          st_coh(dst + 1, y0 * sn + y1 * c);
+        } else {
+          st_coh(LP->vc + (size_t)pos * P.kv_dim + row, y0);
+          st_coh(LP->vc + (size_t)pos * P.kv_dim + row + 1, y1);
+        }
+      };
+      mq_phase<mq_item_tiles(UN * 2), UN * 2, 4, false, MEGA_NW>(ngr, gpb, grp, arr, stage, fin, X, lane, wave);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
+    } else {
       const XStage X = carve_x(smem, P.n, need_l);
       const uint32_t u0 = P.n / RL, u1 = P.kv_dim / RL, total = u0 + 2 * u1;
       auto seg = [&](uint32_t u, int& s, uint32_t& p) {
@@ -499,18 +604,19 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       auto arr = [&] {
         if (l > 0) arrive();
       };
-      auto stage = [&] {
+      auto stage = [&](auto&& pf) {
         if (l > 0) {
           wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
           // x = (base + attproj) + down of the previous layer; publish it
           Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi, pf);
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi, pf);
         } else {
           Src1 src{P.x};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, nullptr, 0, 0, pf);
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -524,10 +630,12 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         for (int r = 0; r < RL; r += 2) {
           const uint32_t row = r0 + r;
           const float y0 = y[r], y1 = y[r + 1];
+          // (loaded for v rows too: a load under the branch would cost the
+          // streaming loop its exact wait counts)
+          const uint32_t i = (row % P.hd) / 2;
+          const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
+          const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
           if (s < 2) {
-            const uint32_t i = (row % P.hd) / 2;
-            const float c = P.rope[((size_t)pos * half + i) * 2 + 0];
-            const float sn = P.rope[((size_t)pos * half + i) * 2 + 1];
             float* dst = s == 0 ? q + row : LP->kc + (size_t)pos * P.kv_dim + row;
             st_coh(dst, y0 * c - y1 * sn);
             st_coh(dst + 1, y0 * sn + y1 * c);
@@ -562,7 +670,29 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);
     }
     // ---- o-projection (the residual add happens where x is next read)
-    {
+    if constexpr (MF) {
+      const XQ X = carve_xq(smem, P.n, MEGA_GPB, MEGA_NW);
+      const int ngr = (int)P.n / 16, gpb = (ngr + (int)nb - 1) / (int)nb;
+      auto grp = [&](int gi, DevMat& M0, DevMat& M1, uint32_t& row0) {
+        M0 = const_mat(&LP->o);
+        M1 = M0;
+        row0 = (uint32_t)gi * 16;
+      };
+      auto stage = [&](auto&& pf) {
+        wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
+        Src1 src{atty};
+        stage_xq_n(src, P.n, nullptr, 0.f, false, X, nullptr, 0, 0, pf);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
+      };
+      auto fin = [&](int gi, int jj, float y0, float y1) {
+        const uint32_t row = (uint32_t)gi * 16 + 2 * jj;
+        st_coh(o_out + row, y0);
+        st_coh(o_out + row + 1, y1);
+      };
+      mq_phase<mq_item_tiles(UN), UN, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
+    } else {
       const XStage X = carve_x(smem, P.n, need_l);
       const uint32_t total = P.n / RL;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
@@ -571,10 +701,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         r0 = (gw + (uint32_t)k * tw) * RL;
         rmax = LP->o.rows;
       };
-      auto stage = [&] {
+      auto stage = [&](auto&& pf) {
         wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
         Src1 src{atty};
-        mega_stage(src, P.n, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
+        mega_stage(src, P.n, nullptr, 0.f, false, X, need_l, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -588,7 +719,27 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     }
     // ---- rmsnorm(base + attproj) + gate/up + SwiGLU
-    {
+    if constexpr (MF) {
+      const XQ X = carve_xq(smem, P.n, MEGA_GPB, MEGA_NW);
+      const int ngr = (int)P.ff / 8, gpb = (ngr + (int)nb - 1) / (int)nb;
+      auto grp = [&](int gi, DevMat& M0, DevMat& M1, uint32_t& row0) {
+        M0 = const_mat(&LP->g);
+        M1 = const_mat(&LP->u);
+        row0 = (uint32_t)gi * 8;
+      };
+      auto stage = [&](auto&& pf) {
+        wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
+        Src2 src{base, o_out};
+        stage_xq_n(src, P.n, LP->ffn_norm, P.eps, true, X, nullptr, 0, 0, pf);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
+      };
+      auto fin = [&](int gi, int jj, float g, float u) {
+        st_coh(h + (size_t)gi * 8 + jj, (g / (1.0f + expf(-g))) * u);
+      };
+      mq_phase<mq_item_tiles(UN * MEGA_NW), UN * MEGA_NW, 1, true, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
+    } else {
       const XStage X = carve_x(smem, P.n, need_l);
       constexpr int PR = RL / 2;
       const uint32_t total = (P.ff + PR - 1) / PR;
@@ -598,10 +749,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         r0 = (gw + (uint32_t)k * tw) * PR;
         rmax = LP->g.rows;
       };
-      auto stage = [&] {
+      auto stage = [&](auto&& pf) {
         wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
         Src2 src{base, o_out};
-        mega_stage(src, P.n, LP->ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0);
+        mega_stage(src, P.n, LP->ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -621,7 +773,29 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     }
     // ---- down-projection (2-row units keep the long rows' double buffer in
     // registers)
-    {
+    if constexpr (MF) {
+      const XQ X = carve_xq(smem, P.ff, MEGA_GPB, MEGA_NW);
+      const int ngr = (int)P.n / 16, gpb = (ngr + (int)nb - 1) / (int)nb;
+      auto grp = [&](int gi, DevMat& M0, DevMat& M1, uint32_t& row0) {
+        M0 = const_mat(&LP->d);
+        M1 = M0;
+        row0 = (uint32_t)gi * 16;
+      };
+      auto stage = [&](auto&& pf) {
+        wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+        Src1 src{h};
+        stage_xq_n(src, P.ff, nullptr, 0.f, false, X, nullptr, 0, 0, pf);
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
+      };
+      auto fin = [&](int gi, int jj, float y0, float y1) {
+        const uint32_t row = (uint32_t)gi * 16 + 2 * jj;
+        st_coh(d_out + row, y0);
+        st_coh(d_out + row + 1, y1);
+      };
+      mq_phase<mq_item_tiles(UF), UF, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
+    } else {
       constexpr int RD = 2;
       const XStage X = carve_x(smem, P.ff, need_l);
       const uint32_t total = P.n / RD;
@@ -631,10 +805,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         r0 = (gw + (uint32_t)k * tw) * RD;
         rmax = LP->d.rows;
       };
-      auto stage = [&] {
+      auto stage = [&](auto&& pf) {
         wait();
+        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
         Src1 src{h};
-        mega_stage(src, P.ff, nullptr, 0.f, false, X, need_l, nullptr, 0, 0);
+        mega_stage(src, P.ff, nullptr, 0.f, false, X, need_l, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
       };
       auto epi = [&](int k, const float(&y)[RD]) {
@@ -681,10 +856,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       r0 = (gw + (uint32_t)k * tw) * RO;
       rmax = P.out_w.rows;
     };
-    auto stage = [&] {
+    auto stage = [&](auto&& pf) {
       wait();
       Src3 src{last, last_o, last_d};
-      mega_stage(src, P.n, P.out_norm, P.eps, true, X, need_o, nullptr, 0, 0);
+      mega_stage(src, P.n, P.out_norm, P.eps, true, X, need_o, nullptr, 0, 0, pf);
       MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
     };
     auto epi = [&](int k, const float(&y)[RO]) {

@@ -132,26 +132,36 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const floa
 
 // Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
 // unit of the wave; epi(k, y) consumes the R row results (every lane holds
-// them).  `arrive` and `stage` are called once by every thread of the block;
-// with `pre` the first item's loads are issued between them (so they overlap
-// whatever `stage` waits for), otherwise after `stage`.
+// them).  `arrive()` and `stage(pf)` are called once by every thread of the
+// block; `stage` calls pf() once, at the point where the first item's weight
+// loads should be issued.  Without `pre` they are issued after `stage`.
 template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class ArriveFn, class StageFn, class EpiFn>
 __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
                                           const float* xs, const float* xsum, int lane, bool pre) {
+  // Every weight load below is issued unconditionally (an idle wave's first
+  // load reads row 0, discarded): the compiler's wait counts then stay exact,
+  // so computing item i waits only for item i's loads, never for item i+1's
+  // (a load under a branch makes the merged count fall back to waiting for
+  // everything).
   MvBuf<FMT, R, U> b0, b1;
-  int nc = 1, iters = 1;
   DevMat A0{}, A1{};
   uint32_t r0 = 0, rmax = 1;
-  if (nunits > 0) {
-    unit(0, A0, A1, r0, rmax);
-    nc = (int)A0.nchunk;
-    iters = (nc + U * TALOS_WAVE - 1) / (U * TALOS_WAVE);
+  unit(0, A0, A1, r0, rmax);
+  const int nc = (int)A0.nchunk;
+  const int iters = (nc + U * TALOS_WAVE - 1) / (U * TALOS_WAVE);
+  if (nunits <= 0) {
+    r0 = 0;
+    rmax = 1;
   }
   arrive();
-  if (pre && nunits > 0) mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
-  stage();
-  if (!pre && nunits > 0) mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
-  const int nitems = nunits * iters;
+  auto pf = [&] { mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane); };
+  if (pre) {
+    stage(pf);
+  } else {
+    stage([] {});
+    pf();
+  }
+  const int nitems = nunits > 0 ? nunits * iters : 0;
   float acc[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) acc[i] = 0.f;
@@ -173,19 +183,27 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arri
       epi(i / iters, y);
     }
   };
-  for (int i = 0; i < nitems; i += 2) {
-    if (i + 1 < nitems) {
-      next_desc(i + 1);
-      mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, ((i + 1) % iters) * U * TALOS_WAVE, lane);
-    }
-    mv_compute<FMT, R, U>(b0, xs, xsum, nc, (i % iters) * U * TALOS_WAVE, lane, acc);
+  auto col = [&](int i) { return (i % iters) * U * TALOS_WAVE; };
+  int i = 0;
+  for (; i + 2 < nitems; i += 2) {  // items i+1 and i+2 exist
+    next_desc(i + 1);
+    mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, col(i + 1), lane);
+    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
     finish(i);
-    if (i + 1 >= nitems) break;
-    if (i + 2 < nitems) {
-      next_desc(i + 2);
-      mv_load<FMT, R, U, PAIR>(b0, N0, N1, nr0, nrmax, ((i + 2) % iters) * U * TALOS_WAVE, lane);
-    }
-    mv_compute<FMT, R, U>(b1, xs, xsum, nc, ((i + 1) % iters) * U * TALOS_WAVE, lane, acc);
+    next_desc(i + 2);
+    mv_load<FMT, R, U, PAIR>(b0, N0, N1, nr0, nrmax, col(i + 2), lane);
+    mv_compute<FMT, R, U>(b1, xs, xsum, nc, col(i + 1), lane, acc);
     finish(i + 1);
+  }
+  if (i + 1 < nitems) {  // two items left
+    next_desc(i + 1);
+    mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, col(i + 1), lane);
+    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
+    finish(i);
+    mv_compute<FMT, R, U>(b1, xs, xsum, nc, col(i + 1), lane, acc);
+    finish(i + 1);
+  } else if (i < nitems) {  // one item left
+    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
+    finish(i);
   }
 }

@@ -96,6 +96,11 @@ struct talos_hip_ctx {
   // launches.  Co-residency is then not promised by the runtime; a barrier
   // that cannot complete times out and the step reports an error.
   bool mega_coop = true;
+  // TALOS_HIP_MFMA=1 runs the Q4_0 layer matvecs of the persistent kernel on
+  // the matrix cores (mfma.h; parity-tested, not yet faster than the vector
+  // path, so off by default).
+  bool allow_mfma = false;
+  bool mega_mfma = false;  // the chosen instantiation runs them on the matrix cores
   MegaParams mp{};
 };
 
@@ -512,22 +517,24 @@ int check_device_err(talos_hip_ctx* c) {
 
 // ---- persistent path
 
-template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL>
-const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl) {
-  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL)
-             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL>
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, bool MF>
+const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, bool mf) {
+  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL && mf == MF)
+             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL, MF>
              : nullptr;
 }
 
-// The instantiations built into the library (the benchmark shapes); other
-// shape/format combinations use the multi-kernel graph path.
-const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl) {
+// The instantiations this library carries: the 7B-shape Q4_0 model on the
+// matrix cores (n = 4096, ff = 14336 -> 4 and 14 tiles per wave) and the
+// vector-ALU streaming path for the tested shapes of each format.
+const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, bool mf) {
   const void* f = nullptr;
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8>(lf, of, un, uf, uo, dpl);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8>(lf, of, un, uf, uo, dpl);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8>(lf, of, un, uf, uo, dpl);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4>(lf, of, un, uf, uo, dpl);
-  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3>(lf, of, un, uf, uo, dpl);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 4, 14, 1, 8, true>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, false>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, false>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, false>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, false>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3, false>(lf, of, un, uf, uo, dpl, mf);
   return f;
 }
 
@@ -565,8 +572,24 @@ int mega_setup(talos_hip_ctx* c) {
     return rc;
   LayerW w0;
   if ((rc = layer_weights(c, 0, &w0))) return rc;
-  const void* fn = mega_kernel_for(lf, wout->mat.fmt, mv_u(w0.q->mat.nchunk), std::min(mv_u(w0.d->mat.nchunk), 2),
-                                   mv_u(wout->mat.nchunk), (int)(c->hd / 16));
+  int dev0 = cf.device;
+  hipDeviceProp_t prop0;
+  HIPCHK(c, hipGetDeviceProperties(&prop0, dev0));
+  const uint32_t nblk = (uint32_t)prop0.multiProcessorCount;
+  auto gpb = [&](uint32_t groups) { return (groups + nblk - 1) / nblk; };
+  // Matrix-core layer phases: Q4_0 layers, rows of whole 1024-element tiles
+  // per wave, at most MEGA_GPB 16-row groups per block in every phase.
+  const bool mf = c->allow_mfma && lf == TALOS_FMT_Q4_0 && cf.n_embd % 1024 == 0 && cf.n_ff % 1024 == 0 &&
+                  c->kv_dim % 16 == 0 && gpb((cf.n_embd + 2 * c->kv_dim) / 16) <= MEGA_GPB &&
+                  gpb(cf.n_ff / 8) <= MEGA_GPB && gpb(cf.n_embd / 16) <= MEGA_GPB;
+  const void* fn = nullptr;
+  if (mf)
+    fn = mega_kernel_for(lf, wout->mat.fmt, (int)(cf.n_embd / 1024), (int)(cf.n_ff / 1024), mv_u(wout->mat.nchunk),
+                         (int)(c->hd / 16), true);
+  c->mega_mfma = fn != nullptr;
+  if (!fn)
+    fn = mega_kernel_for(lf, wout->mat.fmt, mv_u(w0.q->mat.nchunk), std::min(mv_u(w0.d->mat.nchunk), 2),
+                         mv_u(wout->mat.nchunk), (int)(c->hd / 16), false);
   if (!fn) {
     c->mega_ready = true;
     return TALOS_OK;
@@ -585,6 +608,8 @@ int mega_setup(talos_hip_ctx* c) {
   const uint32_t msplit = mega_attn_max_splits(cf.context_length, cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
   const size_t at = mega_attn_lds_floats(c->hd, c->group, msplit) * 4;
   c->mega_lds = std::max(st, at);
+  if (c->mega_mfma)
+    c->mega_lds = std::max(c->mega_lds, xq_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), MEGA_GPB, MEGA_NW));
   if (c->mega_lds > c->max_lds) {
     c->mega_ready = true;
     return TALOS_OK;
@@ -722,6 +747,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->mega_prefetch = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_COOP");
   c->mega_coop = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_MFMA");
+  c->allow_mfma = env && env[0] == '1';
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;

@@ -163,3 +163,20 @@ def test_mistral7b_q4_short_parity(talos, oracle):
     _parity(m, ref, prompt, 4, 1e-3)
     ref.close()
     m.close()
+
+
+def test_mistral7b_q4_matrix_core_parity(talos, oracle, monkeypatch):
+    """The same 7B-shape parity with the layer matvecs of the persistent
+    kernel on the matrix cores (TALOS_HIP_MFMA=1, read when the backend
+    context is created)."""
+    from talos_amd import configs
+    monkeypatch.setenv("TALOS_HIP_MFMA", "1")
+    wl = configs.mistral7b_q4(ctx=256)
+    _step("mistral7b_q4 synth for the matrix-core path")
+    m = talos.Model.synth(wl.spec, nthreads=16)
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=16)
+    prompt = _prompt(wl.spec.seed + 2, 4, wl.spec.vocab_size)
+    _step("mistral7b_q4 matrix-core parity 4 + 4")
+    _parity(m, ref, prompt, 4, 1e-3)
+    ref.close()
+    m.close()
