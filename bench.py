@@ -16,6 +16,12 @@ bytes per step (weights once, K/V read and written, logits) over the mean
 step time.  `cpu_baseline` is the oracle (a C restatement of the
 reference's CPU forward) on a bounded sample of the same model, whose greedy
 tokens are also compared with the GPU's.
+
+--workload lc: the long-context case -- the same 7B shape with every matrix
+in Q8_0, the KV cache filled to 16384 positions by a device prompt feed of
+a uniform random 16384-token prefix (talos_hip_prefill; --lc-fill kv writes
+a seeded K/V state instead), then 64 greedy decode steps at positions
+16384..16447.  Its CPU baseline runs the oracle from the GPU's cache.
 """
 from __future__ import annotations
 
@@ -115,7 +121,11 @@ def matvec_microbench(T) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128, help="timed decode steps (tokens)")
+    ap.add_argument("--workload", choices=("decode", "lc"), default="decode",
+                    help="decode: 7B Q4_0 at KV ctx 4096 (default); lc: 7B Q8_0 after a 16384-token prefix")
+    ap.add_argument("--lc-fill", choices=("prefill", "kv"), default="prefill",
+                    help="lc: fill the 16384-position cache by the device prompt feed or a seeded K/V write")
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (tokens; 128, lc 64)")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before timing")
     ap.add_argument("--cpu-prompt", type=int, default=8, help="prompt tokens of the CPU baseline sample")
     ap.add_argument("--cpu-tokens", type=int, default=32, help="greedy decode tokens of the CPU baseline sample")
@@ -125,6 +135,11 @@ def main() -> int:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               "(the decode path runs on a single MI355X).", file=sys.stderr)
         return 2
+
+    if args.workload == "lc":
+        return run_lc(args)
+    if args.steps is None:
+        args.steps = 128
 
     import numpy as np
 
@@ -258,6 +273,135 @@ def main() -> int:
         "phase_us_per_layer": phases,
         "host_boundary_tok_s": round(pcie_tok_s, 2),
         "matvec_4096x4096": matvec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    model.close()
+    return 0
+
+
+LC_TRAFFIC_FILE = os.path.join("profiles", "k_mega_7b_q8_16k_pmc_traffic.md")
+
+
+def run_lc(args) -> int:
+    """Long-context decode: 7B shape, Q8_0, 16384 cached positions, then
+    --steps (64) greedy steps."""
+    import numpy as np
+
+    import talos_amd as T
+    from talos_amd import configs
+
+    wl = configs.mistral7b_q8_long()
+    spec = wl.spec
+    P = wl.prompt_len
+    steps = wl.decode_steps if args.steps is None else args.steps
+    if steps < 2 or P + max(steps, args.warmup) > spec.context_length:
+        print(f"--steps/--warmup must be in [2, {spec.context_length - P}]", file=sys.stderr)
+        return 2
+    nthreads = host_threads()
+    log(f"generating {wl.name} (seed {spec.seed}) with {nthreads} threads")
+    t = time.perf_counter()
+    model = T.Model.synth(spec, nthreads=nthreads)
+    log(f"  generated in {time.perf_counter() - t:.1f}s")
+    rng = np.random.default_rng(spec.seed + 1)
+    prefix = rng.integers(0, spec.vocab_size, P).astype(np.uint32)
+    t = time.perf_counter()
+    model.forward_token(int(prefix[0]), 0, want_logits=False)  # uploads the weights
+    log(f"  weight upload + first step {time.perf_counter() - t:.1f}s")
+    prefill_tok_s = None
+    if args.lc_fill == "prefill":
+        chunk = 2048
+        t = time.perf_counter()
+        for i in range(0, P, chunk):
+            _, first = model.prefill(prefix[i:i + chunk], i, want_logits=False)
+            log(f"  prefill {min(i + chunk, P)}/{P} positions, {time.perf_counter() - t:.1f}s")
+        prefill_tok_s = P / (time.perf_counter() - t)
+        fill = f"device prompt feed of a uniform random {P}-token prefix ({prefill_tok_s:.1f} tok/s)"
+    else:
+        k = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)
+        v = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)
+        model.kv_write(k, v)
+        del k, v
+        first = int(prefix[-1])
+        fill = f"seeded N(0, 1.28^2) K/V state of {P} positions written to the cache"
+    log(f"cache filled: {fill}")
+    if args.warmup:
+        model.decode_greedy(first, P, args.warmup)
+    t0 = time.perf_counter()
+    toks = model.decode_greedy(first, P, steps)
+    dt = time.perf_counter() - t0
+    tok_s = steps / dt
+    log(f"timed {steps} steps from pos {P}: {dt * 1e3:.2f} ms -> {tok_s:.1f} tok/s")
+    mid = P + steps // 2
+    us, sbytes = model.bench_token(int(toks[steps // 2 - 1]), mid, 16)
+    k_gbs = sbytes / (us * 1e-6) / 1e9
+    log(f"decode step at pos {mid}: {us:.1f} us, {sbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
+    phases = phase_breakdown(model.phase_timeline(int(toks[steps // 2 - 1]), mid), spec.n_layer)
+    log(f"phase us per layer: {phases}")
+    wbytes = configs.bytes_per_token_weights(spec)
+    kvpos = configs.kv_bytes_per_position(spec)
+    tok_bytes = wbytes + kvpos * (P + (steps + 1) / 2.0) + kvpos
+    tok_gbs = tok_bytes * tok_s / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        # Restore the cache to the prefix (the timed run wrote P..P+steps-1,
+        # which the oracle recomputes) and run two greedy steps from it.
+        log(f"CPU baseline: oracle with {nthreads} threads from the GPU's {P}-position cache, 2 decode steps")
+        k, v = model.kv_read(P)
+        ref = O.OracleModel(model.gguf_view(), nthreads=nthreads)
+        ref.set_kv(k, v)
+        del k, v
+        c0 = time.perf_counter()
+        tok, cpu_toks = first, []
+        for i in range(2):
+            tok = O.argmax(ref.forward(tok, P + i))
+            cpu_toks.append(tok)
+        cdt = time.perf_counter() - c0
+        ref.close()
+        match = cpu_toks == [int(x) for x in toks[:2]]
+        log(f"  cpu {2 / cdt:.4f} tok/s over {cdt:.1f}s; greedy tokens match GPU: {match}")
+        cpu = {"value": round(2 / cdt, 5), "unit": "tok/s", "cores": nthreads, "kind": "port",
+               "sample": f"oracle/talos_oracle.c ({nthreads} OpenMP threads; attention is the reference's "
+                         f"serial loop) on the same model: 2 greedy decode steps at pos {P}, {P + 1} from "
+                         f"the GPU's {P}-position cache; greedy tokens identical to the GPU: {match}"}
+
+    traffic = None
+    try:
+        with open(os.path.join(ROOT, LC_TRAFFIC_FILE)) as f:
+            for line in f:
+                if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
+                    traffic = int(line.split("=")[1])
+    except (OSError, ValueError):
+        pass
+    out = {
+        "metric": "decode tok/s batch-1 @7B-shape Q8_0 after a 16384-token prefix (long context)",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"mistral7b_q8_long: 7B shape, Q8_0 matrices (output and embedding too), "
+                               f"KV filled to {P} positions ({fill}), then {steps} greedy steps, "
+                               f"KV capacity {spec.context_length}",
+                   "batch": 1, "prefix_tokens": P, "weights": "Q8_0", "kv": "f32"},
+        "roofline": {"bound": "hbm", "kernel": "k_mega (persistent decode step: 32 layers + output + argmax)",
+                     "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": f"rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE ({LC_TRAFFIC_FILE})",
+                     "bytes_per_launch": int(sbytes), "us_per_launch": round(us, 2), "pos": mid},
+        "token_roofline": {"bytes_per_token": int(tok_bytes), "achieved": round(tok_gbs, 1),
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tok_gbs / HBM_PEAK_GBS, 4),
+                           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / tok_bytes, 1)},
+        "phase_us_per_layer": phases,
+        "prefill_tok_s": None if prefill_tok_s is None else round(prefill_tok_s, 1),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

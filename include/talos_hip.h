@@ -114,6 +114,15 @@ int talos_hip_forward_token(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, fl
 int talos_hip_decode_greedy(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint32_t n_steps,
                             uint32_t* tokens_out);
 
+/* Prompt feed on the device: run tokens[0..n) at positions pos..pos+n-1,
+ * one forward each (the prefill loop of src/main.rs:88-94, Model::step per
+ * prompt token), with each next token taken from a device copy of `tokens`
+ * so the host only launches.  Returns the last step's logits (nullable) and
+ * argmax (nullable), which is the first greedy token.  pos + n must be
+ * <= context_length and every token < vocab_size. */
+int talos_hip_prefill(talos_hip_ctx* ctx, const uint32_t* tokens, uint32_t n, uint32_t pos, float* logits,
+                      uint32_t* argmax);
+
 /* Reset the cache for a new sequence.  Rows are position-indexed, so this
  * only records that no position is valid (the reference's GpuKv needs no
  * clear either, metal/mod.rs:443-454). */
@@ -122,6 +131,11 @@ int talos_hip_kv_reset(talos_hip_ctx* ctx);
 /* Copy `n_pos` positions of the K and V caches of every layer to host
  * buffers laid out [layer][pos][kv_dim] (for tests and state handoff). */
 int talos_hip_kv_read(talos_hip_ctx* ctx, uint32_t n_pos, float* k_out, float* v_out);
+
+/* The inverse: load `n_pos` positions of K and V for every layer from host
+ * buffers laid out [layer][pos][kv_dim] (state handoff, e.g. restoring a
+ * saved long prefix).  No reference counterpart. */
+int talos_hip_kv_write(talos_hip_ctx* ctx, uint32_t n_pos, const float* k, const float* v);
 
 /* Standalone resident matvec, out[rows] = W x: uploads `bytes` under `name`
  * on first use (or on a length change) and runs the fused dequant-matvec.

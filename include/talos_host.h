@@ -47,6 +47,10 @@ int talos_model_dequant_row(const talos_model* m, uint32_t token, float* out);
  * talos_hip_decode_greedy through this model's backend). */
 int talos_model_forward_token(talos_model* m, uint32_t token, size_t pos, float* logits, uint32_t* argmax);
 int talos_model_decode_greedy(talos_model* m, uint32_t token, size_t pos, uint32_t n_steps, uint32_t* tokens);
+/* The prompt loop of src/main.rs:88-94 (Model::step per prompt token) run
+ * through talos_hip_prefill; logits (optional) and argmax of the last token. */
+int talos_model_prefill(talos_model* m, const uint32_t* tokens, uint32_t n, size_t pos, float* logits,
+                        uint32_t* argmax);
 /* The backend context (created and filled with the resident weights on
  * first use). */
 talos_hip_ctx* talos_model_backend(talos_model* m);

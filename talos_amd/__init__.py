@@ -65,6 +65,8 @@ _SIGS = {
     "talos_hip_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, _U32]),
     "talos_hip_kv_reset": (C.c_int, [_P]),
     "talos_hip_kv_read": (C.c_int, [_P, C.c_uint32, _F, _F]),
+    "talos_hip_kv_write": (C.c_int, [_P, C.c_uint32, _F, _F]),
+    "talos_hip_prefill": (C.c_int, [_P, _U32, C.c_uint32, C.c_uint32, _F, _U32]),
     "talos_hip_matvec": (C.c_int, [_P, C.c_char_p, _P, C.c_size_t, C.c_uint32, C.c_size_t, C.c_size_t, _F, _F]),
     "talos_hip_matvec_dev": (C.c_int, [_P, C.c_char_p, _P, _P]),
     "talos_hip_bench_kernel": (C.c_int, [_P, C.c_char_p, C.c_uint32, _F, C.POINTER(C.c_double)]),
@@ -90,6 +92,7 @@ _SIGS = {
     "talos_model_dequant_row": (C.c_int, [_P, C.c_uint32, _F]),
     "talos_model_forward_token": (C.c_int, [_P, C.c_uint32, C.c_size_t, _F, _U32]),
     "talos_model_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_size_t, C.c_uint32, _U32]),
+    "talos_model_prefill": (C.c_int, [_P, _U32, C.c_uint32, C.c_size_t, _F, _U32]),
     "talos_model_backend": (_P, [_P]),
     "talos_synth_model_load": (C.c_int, [C.POINTER(SynthSpecC), C.c_int32, C.c_int32, C.POINTER(_P)]),
     "talos_synth_model_bytes": (C.c_int, [C.POINTER(SynthSpecC), C.c_int32,
@@ -185,8 +188,22 @@ class HipBackend:
         self._check(lib().talos_hip_decode_greedy(self._h, token, pos, n_steps, _u32ptr(out)))
         return out[:n_steps]
 
+    def prefill(self, tokens, pos: int, want_logits=True):
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.cfg.vocab_size, np.float32) if want_logits else None
+        am = C.c_uint32()
+        self._check(lib().talos_hip_prefill(self._h, _u32ptr(t), t.size, pos,
+                                            _fptr(out) if out is not None else None, C.byref(am)))
+        return out, am.value
+
     def kv_reset(self):
         self._check(lib().talos_hip_kv_reset(self._h))
+
+    def kv_write(self, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.ndim == 3
+        self._check(lib().talos_hip_kv_write(self._h, k.shape[1], _fptr(k), _fptr(v)))
 
     def kv_read(self, n_pos: int):
         kvd = self.cfg.n_head_kv * (self.cfg.n_embd // self.cfg.n_head)
@@ -400,6 +417,36 @@ class Model:
         out = np.empty(max(n_steps, 1), np.uint32)
         self._check(lib().talos_model_decode_greedy(self._h, token, pos, n_steps, _u32ptr(out)))
         return out[:n_steps]
+
+    def prefill(self, tokens, pos: int = 0, want_logits: bool = True):
+        """Feed `tokens` at pos.. on the device (main.rs:88-94); returns
+        (last logits or None, last argmax)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.cfg.vocab_size, np.float32) if want_logits else None
+        am = C.c_uint32()
+        self._check(lib().talos_model_prefill(self._h, _u32ptr(t), t.size, pos,
+                                              _fptr(out) if out is not None else None, C.byref(am)))
+        return out, am.value
+
+    def _hip(self, fn, *args):
+        h = self.backend_handle()
+        rc = fn(h, *args)
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
+
+    def kv_read(self, n_pos: int):
+        """K and V caches [layer, pos, kv_dim] of the first n_pos positions."""
+        kvd = self.cfg.n_head_kv * (self.cfg.n_embd // self.cfg.n_head)
+        k = np.empty((self.cfg.n_layer, n_pos, kvd), np.float32)
+        v = np.empty_like(k)
+        self._hip(lib().talos_hip_kv_read, n_pos, _fptr(k), _fptr(v))
+        return k, v
+
+    def kv_write(self, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.ndim == 3 and k.shape[0] == self.cfg.n_layer
+        self._hip(lib().talos_hip_kv_write, k.shape[1], _fptr(k), _fptr(v))
 
     def bench_kernel(self, kind: str, reps: int):
         """(mean launch microseconds, algorithmic bytes per launch) of one

@@ -18,6 +18,12 @@ struct Error : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
 
+// A failed backend call: keeps the talos_status it returned.
+struct BackendError : Error {
+  BackendError(int status, const char* msg) : Error(msg ? msg : "backend error"), status(status) {}
+  int status;
+};
+
 // GGML tensor types (src/gguf/dtype.rs:22-41).
 enum class GgmlType : uint32_t { F32 = 0, Q4_0 = 2, Q8_0 = 8, Q6K = 14 };
 bool ggml_type_from_u32(uint32_t tag, GgmlType* out);

@@ -26,11 +26,11 @@ int guard(talos_model* m, F f) {
   try {
     f();
     return TALOS_OK;
+  } catch (const talos::BackendError& e) {
+    m->err = e.what();
+    return e.status;
   } catch (const std::exception& e) {
     m->err = e.what();
-    const std::string& s = m->err;
-    if (s.find("out of range") != std::string::npos) return TALOS_ERR_TOKEN;
-    if (s.find("context_length") != std::string::npos) return TALOS_ERR_POS;
     return TALOS_ERR_ARG;
   }
 }
@@ -156,6 +156,17 @@ int talos_model_forward_token(talos_model* m, uint32_t token, size_t pos, float*
     std::vector<float> l;
     const uint32_t a = m->m->forward_token(token, pos, logits ? &l : nullptr);
     if (logits) memcpy(logits, l.data(), l.size() * 4);
+    if (argmax) *argmax = a;
+  });
+}
+
+int talos_model_prefill(talos_model* m, const uint32_t* tokens, uint32_t n, size_t pos, float* logits,
+                        uint32_t* argmax) {
+  if (!tokens && n) return TALOS_ERR_ARG;
+  return guard(m, [&] {
+    std::vector<float> l;
+    const uint32_t a = m->m->prefill(tokens, n, pos, logits ? &l : nullptr);
+    if (logits && n) memcpy(logits, l.data(), l.size() * 4);
     if (argmax) *argmax = a;
   });
 }

@@ -7,7 +7,7 @@ namespace talos {
 
 namespace {
 void check(talos_hip_ctx* ctx, int rc) {
-  if (rc != TALOS_OK) throw Error(talos_hip_last_error(ctx));
+  if (rc != TALOS_OK) throw BackendError(rc, talos_hip_last_error(ctx));
 }
 }  // namespace
 
@@ -148,7 +148,8 @@ void Model::cap_context(size_t max_ctx) {
 }
 
 std::vector<float> Model::forward_gpu(uint32_t token, size_t pos) {
-  if (token >= cfg.vocab_size) throw Error("token " + std::to_string(token) + " out of range");
+  if (token >= cfg.vocab_size)
+    throw BackendError(TALOS_ERR_TOKEN, ("token " + std::to_string(token) + " out of range").c_str());
   talos_hip_ctx* c = backend();
   std::vector<float> x(cfg.n_embd), logits(cfg.vocab_size);
   w_.token_embd.dequant_row(token, x.data());  // llama.rs:192-193
@@ -157,7 +158,8 @@ std::vector<float> Model::forward_gpu(uint32_t token, size_t pos) {
 }
 
 std::vector<float> Model::forward_hidden_gpu(uint32_t token, size_t pos) {
-  if (token >= cfg.vocab_size) throw Error("token " + std::to_string(token) + " out of range");
+  if (token >= cfg.vocab_size)
+    throw BackendError(TALOS_ERR_TOKEN, ("token " + std::to_string(token) + " out of range").c_str());
   talos_hip_ctx* c = backend();
   std::vector<float> x(cfg.n_embd), hidden(cfg.n_embd);
   w_.token_embd.dequant_row(token, x.data());
@@ -182,6 +184,14 @@ std::vector<uint32_t> Model::decode_greedy(uint32_t token, size_t pos, uint32_t 
   std::vector<uint32_t> out(n_steps);
   check(c, talos_hip_decode_greedy(c, token, (uint32_t)pos, n_steps, out.data()));
   return out;
+}
+
+uint32_t Model::prefill(const uint32_t* tokens, uint32_t n, size_t pos, std::vector<float>* logits) {
+  talos_hip_ctx* c = backend();
+  uint32_t am = 0;
+  if (logits) logits->resize(cfg.vocab_size);
+  check(c, talos_hip_prefill(c, tokens, n, (uint32_t)pos, logits ? logits->data() : nullptr, &am));
+  return am;
 }
 
 }  // namespace talos

@@ -67,6 +67,9 @@ class Model {
   // Device-side embedding lookup + argmax (no reference counterpart).
   uint32_t forward_token(uint32_t token, size_t pos, std::vector<float>* logits);
   std::vector<uint32_t> decode_greedy(uint32_t token, size_t pos, uint32_t n_steps);
+  // The prompt loop of main.rs:88-94 (step per prompt token) with the
+  // tokens fed on the device; returns the last step's argmax.
+  uint32_t prefill(const uint32_t* tokens, uint32_t n, size_t pos, std::vector<float>* logits);
 
   talos_hip_ctx* backend();
 

@@ -9,7 +9,23 @@
 #include "mvstream.h"
 
 // state[] slots
-enum { ST_POS = 0, ST_TOKEN = 1, ST_ARGMAX = 2, ST_STEP = 3 };
+// ST_NFEED: tokens in tokens[] that a feed (prompt) run consumes in order.
+enum { ST_POS = 0, ST_TOKEN = 1, ST_ARGMAX = 2, ST_STEP = 3, ST_NFEED = 4 };
+
+// Advance the device token state after a step whose argmax is `am`.
+// mode 2 (greedy): the argmax is the next input and is appended to tokens[].
+// mode 3 (feed): the next input is tokens[step + 1] while the feed lasts.
+__device__ __forceinline__ void advance_state(int32_t* state, int32_t* tokens, int32_t am, int mode) {
+  const int32_t step = state[ST_STEP];
+  if (mode == 2) {
+    tokens[step] = am;
+    state[ST_TOKEN] = am;
+  } else if (step + 1 < state[ST_NFEED]) {
+    state[ST_TOKEN] = tokens[step + 1];
+  }
+  state[ST_POS] = state[ST_POS] + 1;
+  state[ST_STEP] = step + 1;
+}
 
 #define TALOS_MAX_GROUP 8
 
@@ -521,8 +537,9 @@ __global__ __launch_bounds__(256) void k_norm(const float* x, const float* w, fl
 
 // ------------------------------------------------------------- k_argmax --
 // argmax by total_cmp, ties to the last index (src/sample.rs:7-14).  With
-// `advance`, the result becomes the next step's token, the position moves
-// on, and the token is appended to `tokens` -- the greedy decode loop runs
+// `advance` (advance_state), the position moves on and the next step's token
+// is set on the device: the argmax itself (2, the greedy loop, which also
+// appends it to `tokens`) or the next fed prompt token (3) -- both loops run
 // without host round trips.
 __global__ __launch_bounds__(1024) void k_argmax(const float* logits, uint32_t n, int32_t* state,
                                                  int32_t* tokens, int advance) {
@@ -558,12 +575,6 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* logits, uint32_t n
         bi = si[w];
       }
     state[ST_ARGMAX] = bi;
-    if (advance) {
-      const int32_t step = state[ST_STEP];
-      tokens[step] = bi;
-      state[ST_TOKEN] = bi;
-      state[ST_POS] = state[ST_POS] + 1;
-      state[ST_STEP] = step + 1;
-    }
+    if (advance) advance_state(state, tokens, bi, advance);
   }
 }

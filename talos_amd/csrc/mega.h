@@ -53,7 +53,7 @@ struct MegaParams {
   uint32_t nsplit, max_chunk;
   int embed;   // 1: x = embedding row of the state token, looked up on the device
   int hidden_only;
-  int argmax;  // 0: none, 1: argmax into state, 2: argmax + advance (greedy loop)
+  int argmax;  // 0: none, 1: argmax into state, 2: + greedy advance, 3: + feed advance (advance_state)
   int prefetch;  // issue each matvec phase's first weight loads before its barrier wait
   uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
 };
@@ -911,13 +911,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     }
     if (P.argmax) {
       P.state[ST_ARGMAX] = i;
-      if (P.argmax == 2) {
-        const int32_t step = P.state[ST_STEP];
-        P.tokens[step] = i;
-        P.state[ST_TOKEN] = i;
-        P.state[ST_POS] = pos + 1;
-        P.state[ST_STEP] = step + 1;
-      }
+      if (P.argmax >= 2) advance_state(P.state, P.tokens, i, P.argmax);
     }
     st_coh_u(epoch_p, ep);
     st_coh_u(done, 0u);

@@ -39,7 +39,11 @@ struct DevWeight {
   const float* f32 = nullptr;  // F32 tensors: the plain row-major data
 };
 
-enum GraphKind { G_LOGITS = 0, G_HIDDEN = 1, G_TOKEN = 2, G_GREEDY = 3, G_COUNT = 4 };
+// G_TOKEN: embedding on the device + argmax; G_GREEDY: + greedy advance;
+// G_FEED: + advance to the next fed prompt token (advance_state).
+enum GraphKind { G_LOGITS = 0, G_HIDDEN = 1, G_TOKEN = 2, G_GREEDY = 3, G_FEED = 4, G_COUNT = 5 };
+static inline bool device_token(int kind) { return kind == G_TOKEN || kind == G_GREEDY || kind == G_FEED; }
+static inline int advance_mode(int kind) { return kind == G_GREEDY ? 2 : (kind == G_FEED ? 3 : 0); }
 
 }  // namespace
 
@@ -74,7 +78,7 @@ struct talos_hip_ctx {
   float* h_out = nullptr;
   int32_t* h_tokens = nullptr;
 
-  hipGraphExec_t graph[G_COUNT] = {nullptr, nullptr, nullptr, nullptr};
+  hipGraphExec_t graph[G_COUNT] = {};
   // TALOS_HIP_GRAPHS=0 enqueues the kernels directly instead of replaying a
   // captured graph (same kernels; used under tracers that mishandle graphs).
   bool use_graphs = true;
@@ -442,7 +446,7 @@ int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
   const auto& cf = c->cfg;
   const uint32_t n = cf.n_embd;
   int rc;
-  if (kind == G_TOKEN || kind == G_GREEDY) {
+  if (device_token(kind)) {
     const DevWeight* emb;
     if ((rc = need_matrix(c, "token_embd.weight", cf.vocab_size, n, &emb))) return rc;
     hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, c->stream, emb->mat, (const int32_t*)c->io, c->x);
@@ -465,9 +469,9 @@ int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
   const DevWeight* wout;
   if ((rc = need_matrix(c, "output.weight", cf.vocab_size, n, &wout))) return rc;
   enq_output(c, wout, onorm);
-  if (kind == G_TOKEN || kind == G_GREEDY)
+  if (device_token(kind))
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, c->stream, c->logits, cf.vocab_size, c->io, c->tokens,
-                       kind == G_GREEDY ? 1 : 0);
+                       advance_mode(kind));
   return TALOS_OK;
 }
 
@@ -673,9 +677,9 @@ int mega_setup(talos_hip_ctx* c) {
 int mega_launch(talos_hip_ctx* c, GraphKind kind, uint64_t* timeline = nullptr) {
   MegaParams P = c->mp;
   P.timeline = timeline;
-  P.embed = kind == G_TOKEN || kind == G_GREEDY;
+  P.embed = device_token(kind);
   P.hidden_only = kind == G_HIDDEN;
-  P.argmax = kind == G_GREEDY ? 2 : (kind == G_TOKEN ? 1 : 0);
+  P.argmax = device_token(kind) ? (kind == G_TOKEN ? 1 : advance_mode(kind)) : 0;
   void* args[] = {&P};
   if (c->mega_coop)
     HIPCHK(c, hipLaunchCooperativeKernel(c->mega_fn, dim3(c->mega_blocks), dim3(MEGA_NT), args,
@@ -954,6 +958,39 @@ int talos_hip_decode_greedy(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint
   return TALOS_OK;
 }
 
+int talos_hip_prefill(talos_hip_ctx* c, const uint32_t* tokens, uint32_t n, uint32_t pos, float* logits,
+                      uint32_t* argmax) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (n == 0) return TALOS_OK;
+  if (!tokens) return fail(c, TALOS_ERR_ARG, "null tokens");
+  if ((uint64_t)pos + n > c->cfg.context_length)
+    return fail(c, TALOS_ERR_POS, "pos %u + %u tokens exceeds context_length %u", pos, n, c->cfg.context_length);
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] >= c->cfg.vocab_size)
+      return fail(c, TALOS_ERR_TOKEN, "tokens[%u] = %u >= vocab_size %u", i, tokens[i], c->cfg.vocab_size);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_FEED, &g))) return rc;
+  for (uint32_t i = 0; i < n; ++i) c->h_tokens[i] = (int32_t)tokens[i];
+  HIPCHK(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+  memset(c->h_io, 0, 64);
+  c->h_io[ST_POS] = (int32_t)pos;
+  c->h_io[ST_TOKEN] = (int32_t)tokens[0];
+  c->h_io[ST_NFEED] = (int32_t)n;
+  HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64, hipMemcpyHostToDevice, c->stream));
+  for (uint32_t i = 0; i < n; ++i)
+    if ((rc = run_step(c, G_FEED, g))) return rc;
+  if (logits)
+    HIPCHK(c, hipMemcpyAsync(c->h_out, c->logits, (size_t)c->cfg.vocab_size * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if ((rc = check_device_err(c))) return rc;
+  if (logits) memcpy(logits, c->h_out, (size_t)c->cfg.vocab_size * 4);
+  if (argmax) *argmax = (uint32_t)c->h_io[ST_ARGMAX];
+  return TALOS_OK;
+}
+
 int talos_hip_kv_reset(talos_hip_ctx* c) { return check_ctx(c); }
 
 int talos_hip_kv_read(talos_hip_ctx* c, uint32_t n_pos, float* k_out, float* v_out) {
@@ -967,6 +1004,22 @@ int talos_hip_kv_read(talos_hip_ctx* c, uint32_t n_pos, float* k_out, float* v_o
   for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
     HIPCHK(c, hipMemcpyAsync(k_out + l * row, c->kc[l], row * 4, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipMemcpyAsync(v_out + l * row, c->vc[l], row * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  return TALOS_OK;
+}
+
+int talos_hip_kv_write(talos_hip_ctx* c, uint32_t n_pos, const float* k, const float* v) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!k || !v) return fail(c, TALOS_ERR_ARG, "null input");
+  if (n_pos > c->cfg.context_length) return fail(c, TALOS_ERR_POS, "n_pos %u > context_length", n_pos);
+  if ((rc = set_device(c))) return rc;
+  if ((rc = alloc_acts(c))) return rc;
+  const size_t row = (size_t)n_pos * c->kv_dim;
+  for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
+    HIPCHK(c, hipMemcpyAsync(c->kc[l], k + l * row, row * 4, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->vc[l], v + l * row, row * 4, hipMemcpyHostToDevice, c->stream));
   }
   HIPCHK(c, hipStreamSynchronize(c->stream));
   return TALOS_OK;
