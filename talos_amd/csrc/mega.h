@@ -249,32 +249,33 @@ __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t
   return gw < total ? (int)((total - gw + tw - 1) / tw) : 0;
 }
 
-// One attention work item: KV head j, positions [t0, t1) of at most
-// MEGA_ATTN_CHUNK (src/model/llama.rs:139-155 for the GQA group of j).  All
-// K, V and q loads are issued together (one memory round trip); K uses 16
-// lanes per position (DPL dims each), V uses 4*DPL lanes per position (a
-// float4 each).  q, the K/V row at `pos` and the slice partials are
-// written once per launch (coherent stores) and read after the barrier or
-// the slice counter that follows the write.  With nsp > 1 slices the last
-// block to finish for head j merges them in slice order.
-#define MEGA_ATTN_CHUNK 128
+// One attention work item: KV head j, positions [t0, t1) of one slice
+// (src/model/llama.rs:139-155 for the GQA group of j).  The slice is walked
+// in sub-chunks of MEGA_ATTN_SUB positions with an online softmax (running
+// max m, running sum l, output rescaled by exp(m_old - m_new)); the K/V rows
+// of sub-chunk c+1 are loaded while sub-chunk c is computed (two register
+// buffers, loads unconditional with clamped rows so the wait counts stay
+// exact).  K uses 16 lanes per position (DPL dims each), V uses 4*DPL lanes
+// per position (a float4 each).  q, the K/V row at `pos` and the slice
+// partials are written once per launch (coherent stores) and read after the
+// barrier or the slice counter that follows the write.  With nsp > 1 slices
+// the last block to finish for head j merges them in slice order.
+#define MEGA_ATTN_SUB 64
 
 static inline __host__ __device__ uint32_t mega_attn_ppr(uint32_t hd) { return MEGA_NT / (hd / 4); }
-// Positions per slice: ceil(seq * n_kv / nblocks) rounded up to 16, within
-// [16, MEGA_ATTN_CHUNK].  The slice count ceil(seq / chunk) is then at most
-// max(ceil(nblocks / n_kv), ceil(seq / MEGA_ATTN_CHUNK)).
+// Positions per slice: ceil(seq * n_kv / nblocks) rounded up to 16 (at
+// least 16), so that the items (KV head x slice) cover about one per block.
+// As chunk >= seq * n_kv / nblocks, the slice count ceil(seq / chunk) is at
+// most ceil(nblocks / n_kv).
 static inline __host__ __device__ int mega_attn_chunk(int seq, uint32_t n_kv, uint32_t nblocks) {
   int c = (int)(((uint64_t)seq * n_kv + nblocks - 1) / nblocks);
   c = (c + 15) & ~15;
-  return c < 16 ? 16 : (c > MEGA_ATTN_CHUNK ? MEGA_ATTN_CHUNK : c);
+  return c < 16 ? 16 : c;
 }
-static inline uint32_t mega_attn_max_splits(uint32_t ctx, uint32_t n_kv, uint32_t nblocks) {
-  const uint32_t a = (nblocks + n_kv - 1) / n_kv, b = (ctx + MEGA_ATTN_CHUNK - 1) / MEGA_ATTN_CHUNK;
-  return a > b ? a : b;
-}
+static inline uint32_t mega_attn_max_splits(uint32_t n_kv, uint32_t nblocks) { return (nblocks + n_kv - 1) / n_kv; }
 static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group, uint32_t nsplit) {
   const size_t ored = (size_t)mega_attn_ppr(hd) * group * hd, comb = 3 * (size_t)nsplit * group;
-  return (size_t)group * hd + (size_t)group * MEGA_ATTN_CHUNK + (ored > comb ? ored : comb) + 64;
+  return (size_t)group * hd + (size_t)group * MEGA_ATTN_SUB + (ored > comb ? ored : comb) + 64;
 }
 
 template <int DPL>
@@ -288,123 +289,149 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
   constexpr int HD = 16 * DPL;            // head_dim
   constexpr int TPP = HD / 4;             // V threads per position
   constexpr int PPR = MEGA_NT / TPP;      // V positions per round
-  constexpr int VR = (MEGA_ATTN_CHUNK + PPR - 1) / PPR;
-  constexpr int KR = MEGA_ATTN_CHUNK / 32;  // K rounds of 32 positions
+  constexpr int VR = (MEGA_ATTN_SUB + PPR - 1) / PPR;
+  constexpr int KR = MEGA_ATTN_SUB / 32;  // K rounds of 32 positions
   const uint32_t group = P.group;
   float* qs = smem;                                  // [group][HD]
-  float* sc = qs + group * HD;                       // [group][CHUNK]
-  float* ored = sc + group * MEGA_ATTN_CHUNK;        // [PPR][group][HD]
-  __shared__ float mh[TALOS_MAX_GROUP], lh[TALOS_MAX_GROUP];
+  float* sc = qs + group * HD;                       // [group][SUB]
+  float* ored = sc + group * MEGA_ATTN_SUB;          // [PPR][group][HD]
+  __shared__ float mh[TALOS_MAX_GROUP], lh[TALOS_MAX_GROUP], ah[TALOS_MAX_GROUP];
   __shared__ int am_last;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int seq = pos + 1;
   const int t0 = split * chunk;
-  const int t1 = min(seq, t0 + chunk);
-  const int len = max(0, t1 - t0);
+  const int t1 = min(seq, t0 + chunk);  // t1 > t0: split < nsp = ceil(seq / chunk)
+  const int len = t1 - t0;
+  const int nsub = (len + MEGA_ATTN_SUB - 1) / MEGA_ATTN_SUB;
   const size_t hoff = (size_t)j * HD;
+  const int dl = lane & 15, slot = wave * 4 + (lane >> 4);  // K: lane group (16 lanes) per position
+  const int vp = tid / TPP, vd = tid % TPP;                 // V: TPP threads per position
+  const int vpc = vp < PPR ? vp : PPR - 1;
 
-  // K: lane group (16 lanes) per position
-  const int dl = lane & 15, slot = wave * 4 + (lane >> 4);
-  float kv[KR][DPL];
-#pragma unroll
-  for (int r = 0; r < KR; ++r) {
-    const int tl = r * 32 + slot;
-    const int t = t0 + (tl < len ? tl : 0);
-    const float* kp = kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
-    if (r * 32 >= len) {  // round past the slice (block-uniform)
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) kv[r][i] = 0.f;
-    } else if constexpr (DPL % 4 == 0) {
-#pragma unroll
-      for (int i = 0; i < DPL; i += 4) {
-        const f4 v = gld4(kp + i);
-        kv[r][i] = v.x;
-        kv[r][i + 1] = v.y;
-        kv[r][i + 2] = v.z;
-        kv[r][i + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) kv[r][i] = gld(kp + i);
-    }
-  }
-  // V: TPP threads per position, a float4 each
-  const int vp = tid / TPP, vd = tid % TPP;
-  f4 vv[VR];
-#pragma unroll
-  for (int r = 0; r < VR; ++r) {
-    const int tl = r * PPR + vp;
-    if (vp < PPR && tl < len) {
-      const float* p = vc + (size_t)(t0 + tl) * P.kv_dim + hoff + vd * 4;
-      vv[r] = gld4(p);
-    } else {
-      vv[r] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-  }
-  // q for the group's heads
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)j * group * HD + i);
-  __syncthreads();
-  ATTN_MARK(0);
-
-  // scores
-  // (a 16-lane group is one DPP row)
-#pragma unroll 1
-  for (int h = 0; h < (int)group; ++h) {
-    float qr[DPL];
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) qr[i] = qs[h * HD + dl * DPL + i];
+  // Rows of sub-chunk c (clamped to the last sub-chunk and the last row of
+  // the slice: out-of-range lanes reload a row of this slice).
+  auto load = [&](float (&kr)[KR][DPL], f4 (&vr)[VR], int c) {
+    const int b = t0 + min(c, nsub - 1) * MEGA_ATTN_SUB;
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-      const int tl = r * 32 + slot;
-      if (r * 32 >= len) break;
-      float d = 0.f;
+      const int t = min(b + r * 32 + slot, t1 - 1);
+      const float* kp = kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
+      if constexpr (DPL % 4 == 0) {
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[i], kv[r][i], d);
-      d = row_sum16(d);
-      if (tl < len && dl == 0) sc[h * MEGA_ATTN_CHUNK + tl] = d * P.scale;
-    }
-  }
-  __syncthreads();
-  // softmax statistics (one wave per head); sc becomes exp(s - m)
-  for (uint32_t h = wave; h < group; h += MEGA_NW) {
-    float mx = -INFINITY;
-    for (int t = lane; t < len; t += 64) mx = fmaxf(mx, sc[h * MEGA_ATTN_CHUNK + t]);
-    mx = wave_max(mx);
-    float l = 0.f;
-    for (int t = lane; t < len; t += 64) {
-      const float e = expf(sc[h * MEGA_ATTN_CHUNK + t] - mx);
-      sc[h * MEGA_ATTN_CHUNK + t] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      mh[h] = mx;
-      lh[h] = l;
-    }
-  }
-  __syncthreads();
-  ATTN_MARK(1);
-  // o[h][4vd..4vd+3] partial over this thread's positions
-  if (vp < PPR) {
-    f4 acc[TALOS_MAX_GROUP];
+        for (int i = 0; i < DPL; i += 4) {
+          const f4 v = gld4(kp + i);
+          kr[r][i] = v.x;
+          kr[r][i + 1] = v.y;
+          kr[r][i + 2] = v.z;
+          kr[r][i + 3] = v.w;
+        }
+      } else {
 #pragma unroll
-    for (int h = 0; h < TALOS_MAX_GROUP; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < DPL; ++i) kr[r][i] = gld(kp + i);
+      }
+    }
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-      const int tl = r * PPR + vp;
-      if (tl < len) {
+      const int t = min(b + r * PPR + vpc, t1 - 1);
+      vr[r] = gld4(vc + (size_t)t * P.kv_dim + hoff + vd * 4);
+    }
+  };
+
+  f4 acc[TALOS_MAX_GROUP];
 #pragma unroll
-        for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
-          if (h < (int)group) {
-            const float p = sc[h * MEGA_ATTN_CHUNK + tl];
-            acc[h].x = __builtin_fmaf(p, vv[r].x, acc[h].x);
-            acc[h].y = __builtin_fmaf(p, vv[r].y, acc[h].y);
-            acc[h].z = __builtin_fmaf(p, vv[r].z, acc[h].z);
-            acc[h].w = __builtin_fmaf(p, vv[r].w, acc[h].w);
+  for (int h = 0; h < TALOS_MAX_GROUP; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // Online softmax over sub-chunk c held in (kr, vr).
+  auto compute = [&](const float (&kr)[KR][DPL], const f4 (&vr)[VR], int c) {
+    const int slen = min(MEGA_ATTN_SUB, len - c * MEGA_ATTN_SUB);
+    // scores (a 16-lane group is one DPP row)
+#pragma unroll 1
+    for (int h = 0; h < (int)group; ++h) {
+      float qr[DPL];
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) qr[i] = qs[h * HD + dl * DPL + i];
+#pragma unroll
+      for (int r = 0; r < KR; ++r) {
+        const int tl = r * 32 + slot;
+        if (r * 32 >= slen) break;
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[i], kr[r][i], d);
+        d = row_sum16(d);
+        if (tl < slen && dl == 0) sc[h * MEGA_ATTN_SUB + tl] = d * P.scale;
+      }
+    }
+    __syncthreads();
+    // running statistics (one wave per head); sc becomes exp(s - m_new)
+    for (uint32_t h = wave; h < group; h += MEGA_NW) {
+      float mx = -INFINITY;
+      for (int t = lane; t < slen; t += 64) mx = fmaxf(mx, sc[h * MEGA_ATTN_SUB + t]);
+      mx = wave_max(mx);
+      const float m_old = c == 0 ? -INFINITY : mh[h];
+      const float m_new = fmaxf(m_old, mx);
+      float l = 0.f;
+      for (int t = lane; t < slen; t += 64) {
+        const float e = expf(sc[h * MEGA_ATTN_SUB + t] - m_new);
+        sc[h * MEGA_ATTN_SUB + t] = e;
+        l += e;
+      }
+      l = wave_sum(l);
+      if (lane == 0) {
+        const float a = c == 0 ? 0.f : expf(m_old - m_new);
+        ah[h] = a;
+        lh[h] = c == 0 ? l : __builtin_fmaf(lh[h], a, l);
+        mh[h] = m_new;
+      }
+    }
+    __syncthreads();
+    // o[h][4vd..4vd+3] over this thread's positions, rescaled
+    if (vp < PPR) {
+#pragma unroll
+      for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
+        if (h < (int)group) {
+          const float a = ah[h];
+          acc[h].x *= a;
+          acc[h].y *= a;
+          acc[h].z *= a;
+          acc[h].w *= a;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < VR; ++r) {
+        const int tl = r * PPR + vp;
+        if (tl < slen) {
+#pragma unroll
+          for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
+            if (h < (int)group) {
+              const float p = sc[h * MEGA_ATTN_SUB + tl];
+              acc[h].x = __builtin_fmaf(p, vr[r].x, acc[h].x);
+              acc[h].y = __builtin_fmaf(p, vr[r].y, acc[h].y);
+              acc[h].z = __builtin_fmaf(p, vr[r].z, acc[h].z);
+              acc[h].w = __builtin_fmaf(p, vr[r].w, acc[h].w);
+            }
           }
         }
       }
     }
+    __syncthreads();  // sc and ah are rewritten by the next sub-chunk
+  };
+
+  float kA[KR][DPL], kB[KR][DPL];
+  f4 vA[VR], vB[VR];
+  load(kA, vA, 0);
+  // q for the group's heads
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)j * group * HD + i);
+  __syncthreads();
+  ATTN_MARK(0);
+  for (int c = 0; c < nsub; c += 2) {
+    load(kB, vB, c + 1);
+    compute(kA, vA, c);
+    if (c + 1 >= nsub) break;
+    load(kA, vA, c + 2);
+    compute(kB, vB, c + 1);
+  }
+  ATTN_MARK(1);
+  if (vp < PPR) {
 #pragma unroll
     for (int h = 0; h < TALOS_MAX_GROUP; ++h)
       if (h < (int)group) *reinterpret_cast<f4*>(ored + ((size_t)vp * group + h) * HD + vd * 4) = acc[h];
@@ -467,18 +494,23 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
       lh[tid] = Ls;
     }
     __syncthreads();
+    // 16 slices per memory round trip (clamped loads, weight applied only
+    // to live slices), summed in slice order
+    constexpr int MB = 16;
     for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
       const uint32_t h = i / HD, dd = i % HD;
       float O = 0.f;
-      int s = 0;
-      for (; s + 4 <= nsp; s += 4) {
-        float o4[4];
+      for (int s0 = 0; s0 < nsp; s0 += MB) {
+        float o16[MB];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = gld(parts + ((size_t)(s + r) * group + h) * pstride + dd);
+        for (int r = 0; r < MB; ++r) {
+          const int s = min(s0 + r, nsp - 1);
+          o16[r] = gld(parts + ((size_t)s * group + h) * pstride + dd);
+        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) O = __builtin_fmaf(o4[r], cw[(s + r) * group + h], O);
+        for (int r = 0; r < MB; ++r)
+          if (s0 + r < nsp) O = __builtin_fmaf(o16[r], cw[(s0 + r) * group + h], O);
       }
-      for (; s < nsp; ++s) O = __builtin_fmaf(gld(parts + ((size_t)s * group + h) * pstride + dd), cw[s * group + h], O);
       st_coh(atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
@@ -653,8 +685,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     {
       grid_barrier(G, ++ep);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 2);
-      // slices of 16..MEGA_ATTN_CHUNK positions, sized so that the items
-      // (KV head x slice) cover about one per block
+      // slices of >= 16 positions, sized so that the items (KV head x
+      // slice) cover about one per block
       const int seq = pos + 1;
       const int chunk = mega_attn_chunk(seq, P.n_kv, nb);
       const int nsp = (seq + chunk - 1) / chunk;

@@ -609,7 +609,7 @@ int mega_setup(talos_hip_ctx* c) {
   }
   // LDS: x staging for the widest input, or the attention scratch.
   const size_t st = stage_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), 3);
-  const uint32_t msplit = mega_attn_max_splits(cf.context_length, cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
+  const uint32_t msplit = mega_attn_max_splits(cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
   const size_t at = mega_attn_lds_floats(c->hd, c->group, msplit) * 4;
   c->mega_lds = std::max(st, at);
   if (c->mega_mfma)
@@ -668,7 +668,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.tokens = c->tokens;
   P.sync = c->d_sync;
   P.nsplit = msplit;
-  P.max_chunk = MEGA_ATTN_CHUNK;
+  P.max_chunk = MEGA_ATTN_SUB;
   c->mega_fn = fn;
   c->mega_ready = true;
   return TALOS_OK;
