@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
 }
 
 // --------------------------------------------------------------- k_rows --
@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
 }
 
 // ------------------------------------------------------------- k_gateup --
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, true>(nunits, unit, [] {}, stage, epi, X.xs[MvT<FMT>::L], X.xsum, lane, true);
+  mv_stream<FMT, R, U, true>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
 }
 
 // ---------------------------------------------------------------- k_attn --

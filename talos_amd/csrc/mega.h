@@ -214,6 +214,45 @@ __device__ __forceinline__ void stage_xq_n(Src src, int n, const float* w, float
     stage_xq<4, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
 }
 
+// Matvec modes of the persistent kernel: f32 x on the vector ALUs, Q4_0 on
+// the matrix cores (mfma.h), or int8-plane x with v_dot4 on the vector ALUs
+// (mv_compute for XI; Q4_0 / Q8_0 layers).
+enum { MEGA_MM_F32 = 0, MEGA_MM_MFMA = 1, MEGA_MM_DOT4 = 2 };
+
+// The staged x of a vector-ALU matvec phase: f32 (carve_x / mega_stage) or
+// int8 planes (carve_xq / stage_xq with the bank-conflict-free layout).
+template <bool IQ>
+struct MegaX {
+  XStage X;
+  int need;
+  __device__ __forceinline__ MegaX(float* smem, int n, int need_) : X(carve_x(smem, n, need_)), need(need_) {}
+  template <class Src, class After>
+  __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
+                                        int hi, After after) const {
+    mega_stage(src, n, w, eps, norm, X, need, pub, lo, hi, after);
+  }
+  __device__ __forceinline__ XF src(int layout) const { return XF{X.xs[layout], X.xsum}; }
+};
+template <>
+struct MegaX<true> {
+  XQ X;
+  __device__ __forceinline__ MegaX(float* smem, int n, int) : X(carve_xq(smem, n, MEGA_GPB, MEGA_NW)) {}
+  template <class Src, class After>
+  __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
+                                        int hi, After after) const {
+    const int n8 = n >> 3;
+    if (n8 <= MEGA_NT)
+      stage_xq<1, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+    else if (n8 <= 2 * MEGA_NT)
+      stage_xq<2, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+    else
+      stage_xq<4, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+  }
+  __device__ __forceinline__ XI src(int) const {
+    return XI{reinterpret_cast<const uint8_t*>(X.pl), X.bs, X.nb};
+  }
+};
+
 // x[e..e+3] of one array, of a + b, or of (a + b) + c: the residual stream
 // is kept as the layer's base plus the o-projection and down-projection
 // outputs, summed in the order of src/model/llama.rs:159-161, 174-176.
@@ -522,9 +561,12 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
 
 // MF: the layer matvecs (Q4_0) run on the matrix cores (mfma.h); UN and UF
 // are then the tiles per wave of the n- and ff-wide rows (cols / 1024).
-template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, bool MF>
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, int MM>
 __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   extern __shared__ float smem[];
+  constexpr bool MF = MM == MEGA_MM_MFMA;
+  constexpr bool IQ = MM == MEGA_MM_DOT4;
+  constexpr bool IQO = IQ && (OF == TALOS_FMT_Q4_0 || OF == TALOS_FMT_Q8_0);  // the head too
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t nb = gridDim.x;
   const uint32_t gw = blockIdx.x * MEGA_NW + wave, tw = nb * MEGA_NW;
@@ -618,7 +660,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UN * 2), UN * 2, 4, false, MEGA_NW>(ngr, gpb, grp, arr, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
     } else {
-      const XStage X = carve_x(smem, P.n, need_l);
+      const MegaX<IQ> X(smem, P.n, need_l);
       const uint32_t u0 = P.n / RL, u1 = P.kv_dim / RL, total = u0 + 2 * u1;
       auto seg = [&](uint32_t u, int& s, uint32_t& p) {
         s = u < u0 ? 0 : (u < u0 + u1 ? 1 : 2);
@@ -642,13 +684,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
           // x = (base + attproj) + down of the previous layer; publish it
           Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf);
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, base, pub_lo, pub_hi, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf);
         } else {
           Src1 src{P.x};
-          mega_stage(src, P.n, LP->attn_norm, P.eps, true, X, need_l, nullptr, 0, 0, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, nullptr, 0, 0, pf);
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -677,7 +719,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arr, stage, epi, X.xs[LL], X.xsum, lane,
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arr, stage, epi, X.src(LL), lane,
                                    pre && l > 0);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
     }
@@ -725,7 +767,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UN), UN, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     } else {
-      const XStage X = carve_x(smem, P.n, need_l);
+      const MegaX<IQ> X(smem, P.n, need_l);
       const uint32_t total = P.n / RL;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
         A0 = const_mat(&LP->o);
@@ -737,7 +779,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         wait();
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
         Src1 src{atty};
-        mega_stage(src, P.n, nullptr, 0.f, false, X, need_l, nullptr, 0, 0, pf);
+        X.stage(src, P.n, nullptr, 0.f, false, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -746,7 +788,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
 #pragma unroll
         for (int r = 0; r < RL; ++r) st_coh(o_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                    pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     }
@@ -772,7 +814,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UN * MEGA_NW), UN * MEGA_NW, 1, true, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     } else {
-      const XStage X = carve_x(smem, P.n, need_l);
+      const MegaX<IQ> X(smem, P.n, need_l);
       constexpr int PR = RL / 2;
       const uint32_t total = (P.ff + PR - 1) / PR;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
@@ -785,7 +827,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         wait();
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
         Src2 src{base, o_out};
-        mega_stage(src, P.n, LP->ffn_norm, P.eps, true, X, need_l, nullptr, 0, 0, pf);
+        X.stage(src, P.n, LP->ffn_norm, P.eps, true, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -799,7 +841,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                   pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
@@ -829,7 +871,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     } else {
       constexpr int RD = 2;
-      const XStage X = carve_x(smem, P.ff, need_l);
+      const MegaX<IQ> X(smem, P.ff, need_l);
       const uint32_t total = P.n / RD;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
         A0 = const_mat(&LP->d);
@@ -841,7 +883,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         wait();
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
         Src1 src{h};
-        mega_stage(src, P.ff, nullptr, 0.f, false, X, need_l, nullptr, 0, 0, pf);
+        X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
       };
       auto epi = [&](int k, const float(&y)[RD]) {
@@ -850,7 +892,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
 #pragma unroll
         for (int r = 0; r < RD; ++r) st_coh(d_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LL], X.xsum, lane,
+      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                    pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     }
@@ -880,7 +922,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       }
     }
   } else {
-    const XStage X = carve_x(smem, P.n, need_o);
+    const MegaX<IQO> X(smem, P.n, need_o);
     const uint32_t total = (P.vocab + RO - 1) / RO;
     auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
       A0 = P.out_w;
@@ -891,7 +933,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     auto stage = [&](auto&& pf) {
       wait();
       Src3 src{last, last_o, last_d};
-      mega_stage(src, P.n, P.out_norm, P.eps, true, X, need_o, nullptr, 0, 0, pf);
+      X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf);
       MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
     };
     auto epi = [&](int k, const float(&y)[RO]) {
@@ -909,7 +951,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         }
       }
     };
-    mv_stream<OF, RO, UO, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.xs[LO], X.xsum, lane, pre);
+    mv_stream<OF, RO, UO, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LO), lane, pre);
     MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 1);
   }
   // per-block best, then the last block to finish reduces and advances state

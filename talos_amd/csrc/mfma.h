@@ -64,7 +64,10 @@ __device__ __forceinline__ float rne(float t) { return __builtin_rintf(t); }
 // elements per round (4 threads = one block).  All loads are issued first,
 // then after() (the matvec's first weight loads), then the arithmetic.  The
 // block publishes its raw x slice [pub_lo, pub_hi) to `pub` (coherent).
-template <int NR, int NT, class Src, class After>
+// Plane layout: [3][nb][32] bytes, or with SPLIT [3][2][nb] 16-byte words
+// (word h of block b at (h * nb + b) * 16: a wave reading one block per lane
+// touches consecutive words, free of LDS bank conflicts).
+template <int NR, int NT, bool SPLIT = false, class Src, class After>
 __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict__ w, float eps, bool norm,
                                          const XQ& X, float* pub, int pub_lo, int pub_hi, After after) {
   int tid = threadIdx.x;
@@ -153,9 +156,10 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
     if (ok) {
       const int blk = g8 >> 2, off = (g8 & 3) * 8;
       const size_t plane = (size_t)X.nb * 32;
-      *reinterpret_cast<uint2*>(X.pl + (size_t)blk * 32 + off) = uint2{pa[0], pa[1]};
-      *reinterpret_cast<uint2*>(X.pl + plane + (size_t)blk * 32 + off) = uint2{pb[0], pb[1]};
-      *reinterpret_cast<uint2*>(X.pl + 2 * plane + (size_t)blk * 32 + off) = uint2{pc[0], pc[1]};
+      const size_t at = SPLIT ? ((size_t)(off >> 4) * X.nb + blk) * 16 + (off & 15) : (size_t)blk * 32 + off;
+      *reinterpret_cast<uint2*>(X.pl + at) = uint2{pa[0], pa[1]};
+      *reinterpret_cast<uint2*>(X.pl + plane + at) = uint2{pb[0], pb[1]};
+      *reinterpret_cast<uint2*>(X.pl + 2 * plane + at) = uint2{pc[0], pc[1]};
       if ((g8 & 3) == 0) X.bs[blk] = float2{am / 127.f, sm};
     }
   }

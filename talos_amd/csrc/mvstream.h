@@ -74,10 +74,26 @@ __device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, c
   }
 }
 
+// The staged x a matvec reads: f32 values (XF: xs in the xidx layout of
+// the format, xsum per 16 elements), or int8 planes (XI, Q4_0/Q8_0 only:
+// the [3][2][nb] 16-byte words and (s, sum) per 32-element block of
+// stage_xq with SPLIT).
+struct XF {
+  const float* xs;
+  const float* xsum;
+};
+struct XI {
+  const uint8_t* pl;
+  const float2* bs;
+  int nb;
+};
+
 // acc[i] += <row slot i, x> over this item's chunks.
 template <uint32_t FMT, int R, int U>
-__device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const float* xs, const float* xsum, int nc,
-                                           int c0, int lane, float (&acc)[R]) {
+__device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XF& X, int nc, int c0, int lane,
+                                           float (&acc)[R]) {
+  const float* xs = X.xs;
+  const float* xsum = X.xsum;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int c = c0 + u * TALOS_WAVE + lane;
@@ -130,14 +146,90 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const floa
   }
 }
 
+// acc[i] += <row slot i, x> with x as three int8 planes:
+// x_e = s_b * (a_e + b_e/254 + c_e/254^2) for the elements e of block b
+// (error <= 2^-24 * max|x_b|, f32-level).  The integer piece dots are exact
+// (v_dot4_i32_i8: Q4_0 nibbles 0..15 or Q8_0 quants times plane bytes);
+// the block then contributes d * (s/254 * ((254 A + B) + C/254) - off * sum_b)
+// with off = 8 for Q4_0 (its -8, src/gguf/dtype.rs:83-90) and 0 for Q8_0.
+__device__ __forceinline__ int dot4_i8(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+template <uint32_t FMT, int R, int U>
+__device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XI& X, int nc, int c0, int lane,
+                                           float (&acc)[R]) {
+  static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "int8-plane x is for Q4_0 / Q8_0");
+  constexpr float k254 = 1.0f / 254.0f;
+  const size_t plane = (size_t)X.nb * 32;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * TALOS_WAVE + lane;
+    const bool ok = c < nc;
+    const int cc = ok ? c : nc - 1;
+    u4 pw[3][2];
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        pw[p][h] = *reinterpret_cast<const u4*>(X.pl + p * plane + ((size_t)h * X.nb + cc) * 16);
+    const float2 sx = X.bs[cc];
+    const float s254 = sx.x * k254;
+    const float off = FMT == TALOS_FMT_Q4_0 ? -8.f * sx.y : 0.f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      uint32_t w[8];
+      if (FMT == TALOS_FMT_Q4_0) {
+        const u4 q = B.q[i][u][0];
+        w[0] = q.x & 0x0F0F0F0Fu;
+        w[1] = q.y & 0x0F0F0F0Fu;
+        w[2] = q.z & 0x0F0F0F0Fu;
+        w[3] = q.w & 0x0F0F0F0Fu;
+        w[4] = (q.x >> 4) & 0x0F0F0F0Fu;
+        w[5] = (q.y >> 4) & 0x0F0F0F0Fu;
+        w[6] = (q.z >> 4) & 0x0F0F0F0Fu;
+        w[7] = (q.w >> 4) & 0x0F0F0F0Fu;
+      } else {  // the device layout keeps Q8_0 quants biased by 128 (q ^ 0x80)
+        const u4 q0 = B.q[i][u][0], q1 = B.q[i][u][MvT<FMT>::QW - 1];
+        w[0] = q0.x ^ 0x80808080u;
+        w[1] = q0.y ^ 0x80808080u;
+        w[2] = q0.z ^ 0x80808080u;
+        w[3] = q0.w ^ 0x80808080u;
+        w[4] = q1.x ^ 0x80808080u;
+        w[5] = q1.y ^ 0x80808080u;
+        w[6] = q1.z ^ 0x80808080u;
+        w[7] = q1.w ^ 0x80808080u;
+      }
+      int dp[3];
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        int a = 0;
+        a = dot4_i8(w[0], pw[p][0].x, a);
+        a = dot4_i8(w[1], pw[p][0].y, a);
+        a = dot4_i8(w[2], pw[p][0].z, a);
+        a = dot4_i8(w[3], pw[p][0].w, a);
+        a = dot4_i8(w[4], pw[p][1].x, a);
+        a = dot4_i8(w[5], pw[p][1].y, a);
+        a = dot4_i8(w[6], pw[p][1].z, a);
+        a = dot4_i8(w[7], pw[p][1].w, a);
+        dp[p] = a;
+      }
+      // |dp[0]| <= 32 * 128 * 127, so 254 * dp[0] + dp[1] fits an int32
+      const float t = __builtin_fmaf((float)dp[2], k254, (float)(dp[0] * 254 + dp[1]));
+      const float d = ok ? f16_to_f32((uint16_t)B.a[i][u]) : 0.f;
+      acc[i] = __builtin_fmaf(d, __builtin_fmaf(s254, t, off), acc[i]);
+    }
+  }
+}
+
 // Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
 // unit of the wave; epi(k, y) consumes the R row results (every lane holds
 // them).  `arrive()` and `stage(pf)` are called once by every thread of the
 // block; `stage` calls pf() once, at the point where the first item's weight
 // loads should be issued.  Without `pre` they are issued after `stage`.
-template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class ArriveFn, class StageFn, class EpiFn>
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class ArriveFn, class StageFn, class EpiFn, class XS>
 __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
-                                          const float* xs, const float* xsum, int lane, bool pre) {
+                                          const XS& xs, int lane, bool pre) {
   // Every weight load below is issued unconditionally (an idle wave's first
   // load reads row 0, discarded): the compiler's wait counts then stay exact,
   // so computing item i waits only for item i's loads, never for item i+1's
@@ -188,22 +280,22 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arri
   for (; i + 2 < nitems; i += 2) {  // items i+1 and i+2 exist
     next_desc(i + 1);
     mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, col(i + 1), lane);
-    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
+    mv_compute<FMT, R, U>(b0, xs, nc, col(i), lane, acc);
     finish(i);
     next_desc(i + 2);
     mv_load<FMT, R, U, PAIR>(b0, N0, N1, nr0, nrmax, col(i + 2), lane);
-    mv_compute<FMT, R, U>(b1, xs, xsum, nc, col(i + 1), lane, acc);
+    mv_compute<FMT, R, U>(b1, xs, nc, col(i + 1), lane, acc);
     finish(i + 1);
   }
   if (i + 1 < nitems) {  // two items left
     next_desc(i + 1);
     mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, col(i + 1), lane);
-    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
+    mv_compute<FMT, R, U>(b0, xs, nc, col(i), lane, acc);
     finish(i);
-    mv_compute<FMT, R, U>(b1, xs, xsum, nc, col(i + 1), lane, acc);
+    mv_compute<FMT, R, U>(b1, xs, nc, col(i + 1), lane, acc);
     finish(i + 1);
   } else if (i < nitems) {  // one item left
-    mv_compute<FMT, R, U>(b0, xs, xsum, nc, col(i), lane, acc);
+    mv_compute<FMT, R, U>(b0, xs, nc, col(i), lane, acc);
     finish(i);
   }
 }

@@ -105,6 +105,10 @@ struct talos_hip_ctx {
   // path, so off by default).
   bool allow_mfma = false;
   bool mega_mfma = false;  // the chosen instantiation runs them on the matrix cores
+  // TALOS_HIP_DOT4=0 keeps x in f32 for the Q4_0 / Q8_0 layer matvecs of the
+  // persistent kernel instead of int8 planes with v_dot4 (the default).
+  bool allow_dot4 = true;
+  int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
   MegaParams mp{};
 };
 
@@ -521,24 +525,30 @@ int check_device_err(talos_hip_ctx* c) {
 
 // ---- persistent path
 
-template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, bool MF>
-const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, bool mf) {
-  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL && mf == MF)
-             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL, MF>
+template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, int MM>
+const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, int mm) {
+  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL && mm == MM)
+             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL, MM>
              : nullptr;
 }
 
 // The instantiations this library carries: the 7B-shape Q4_0 model on the
-// matrix cores (n = 4096, ff = 14336 -> 4 and 14 tiles per wave) and the
-// vector-ALU streaming path for the tested shapes of each format.
-const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, bool mf) {
+// matrix cores (n = 4096, ff = 14336 -> 4 and 14 tiles per wave), and the
+// vector-ALU streaming path with int8-plane x (Q4_0 / Q8_0) or f32 x for the
+// tested shapes of each format.
+const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, int mm) {
+  constexpr int F = MEGA_MM_F32, M = MEGA_MM_MFMA, D = MEGA_MM_DOT4;
   const void* f = nullptr;
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 4, 14, 1, 8, true>(lf, of, un, uf, uo, dpl, mf);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, false>(lf, of, un, uf, uo, dpl, mf);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, false>(lf, of, un, uf, uo, dpl, mf);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, false>(lf, of, un, uf, uo, dpl, mf);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, false>(lf, of, un, uf, uo, dpl, mf);
-  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3, false>(lf, of, un, uf, uo, dpl, mf);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 4, 14, 1, 8, M>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, F>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, F>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3, F>(lf, of, un, uf, uo, dpl, mm);
   return f;
 }
 
@@ -587,13 +597,19 @@ int mega_setup(talos_hip_ctx* c) {
                   c->kv_dim % 16 == 0 && gpb((cf.n_embd + 2 * c->kv_dim) / 16) <= MEGA_GPB &&
                   gpb(cf.n_ff / 8) <= MEGA_GPB && gpb(cf.n_embd / 16) <= MEGA_GPB;
   const void* fn = nullptr;
-  if (mf)
+  c->mega_mode = MEGA_MM_F32;
+  if (mf) {
     fn = mega_kernel_for(lf, wout->mat.fmt, (int)(cf.n_embd / 1024), (int)(cf.n_ff / 1024), mv_u(wout->mat.nchunk),
-                         (int)(c->hd / 16), true);
+                         (int)(c->hd / 16), MEGA_MM_MFMA);
+    if (fn) c->mega_mode = MEGA_MM_MFMA;
+  }
   c->mega_mfma = fn != nullptr;
-  if (!fn)
-    fn = mega_kernel_for(lf, wout->mat.fmt, mv_u(w0.q->mat.nchunk), std::min(mv_u(w0.d->mat.nchunk), 2),
-                         mv_u(wout->mat.nchunk), (int)(c->hd / 16), false);
+  const int un = mv_u(w0.q->mat.nchunk), uf = std::min(mv_u(w0.d->mat.nchunk), 2), uo = mv_u(wout->mat.nchunk);
+  if (!fn && c->allow_dot4 && (lf == TALOS_FMT_Q4_0 || lf == TALOS_FMT_Q8_0)) {
+    fn = mega_kernel_for(lf, wout->mat.fmt, un, uf, uo, (int)(c->hd / 16), MEGA_MM_DOT4);
+    if (fn) c->mega_mode = MEGA_MM_DOT4;
+  }
+  if (!fn) fn = mega_kernel_for(lf, wout->mat.fmt, un, uf, uo, (int)(c->hd / 16), MEGA_MM_F32);
   if (!fn) {
     c->mega_ready = true;
     return TALOS_OK;
@@ -612,7 +628,7 @@ int mega_setup(talos_hip_ctx* c) {
   const uint32_t msplit = mega_attn_max_splits(cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
   const size_t at = mega_attn_lds_floats(c->hd, c->group, msplit) * 4;
   c->mega_lds = std::max(st, at);
-  if (c->mega_mfma)
+  if (c->mega_mode != MEGA_MM_F32)
     c->mega_lds = std::max(c->mega_lds, xq_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), MEGA_GPB, MEGA_NW));
   if (c->mega_lds > c->max_lds) {
     c->mega_ready = true;
@@ -753,6 +769,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->mega_coop = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_MFMA");
   c->allow_mfma = env && env[0] == '1';
+  env = getenv("TALOS_HIP_DOT4");
+  c->allow_dot4 = !(env && env[0] == '0');
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;

@@ -180,3 +180,18 @@ def test_mistral7b_q4_matrix_core_parity(talos, oracle, monkeypatch):
     _parity(m, ref, prompt, 4, 1e-3)
     ref.close()
     m.close()
+
+
+def test_gqa_q8_f32_x_parity(talos, oracle, monkeypatch):
+    """The vector-ALU layer matvecs with f32 x (TALOS_HIP_DOT4=0, read when
+    the backend context is created) instead of the default int8-plane x."""
+    from talos_amd import configs
+    monkeypatch.setenv("TALOS_HIP_DOT4", "0")
+    wl = configs.gqa_q8()
+    _step("gqa_q8 with f32 x: 16-token prompt + 32 greedy steps")
+    m = talos.Model.synth(wl.spec)
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=8)
+    prompt = _prompt(wl.spec.seed + 3, wl.prompt_len, wl.spec.vocab_size)
+    _parity(m, ref, prompt, 32, 1e-3)
+    ref.close()
+    m.close()
