@@ -312,9 +312,8 @@ static inline __host__ __device__ int mega_attn_chunk(int seq, uint32_t n_kv, ui
   return c < 16 ? 16 : c;
 }
 static inline uint32_t mega_attn_max_splits(uint32_t n_kv, uint32_t nblocks) { return (nblocks + n_kv - 1) / n_kv; }
-static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group, uint32_t nsplit) {
-  const size_t ored = (size_t)mega_attn_ppr(hd) * group * hd, comb = 3 * (size_t)nsplit * group;
-  return (size_t)group * hd + (size_t)group * MEGA_ATTN_SUB + (ored > comb ? ored : comb) + 64;
+static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group) {
+  return (size_t)group * hd + (size_t)group * MEGA_ATTN_SUB + (size_t)mega_attn_ppr(hd) * group * hd + 64;
 }
 
 template <int DPL>
@@ -512,45 +511,39 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
   ATTN_MARK(3);
   if (am_last) {
     const float* parts = part + (size_t)j * P.nsplit * group * pstride;
-    float* cm = sc;  // reuses the score / reduction scratch
-    float* cl = cm + nsp * group;
-    float* cw = cl + nsp * group;
-    for (int i = tid; i < nsp * (int)group; i += MEGA_NT) {
-      const int s = i / (int)group, h = i % (int)group;
-      cm[i] = gld(parts + ((size_t)s * group + h) * pstride + HD);
-      cl[i] = gld(parts + ((size_t)s * group + h) * pstride + HD + 1);
-    }
-    __syncthreads();
-    if (tid < (int)group) {
-      float M = -INFINITY;
-      for (int s = 0; s < nsp; ++s) M = fmaxf(M, cm[s * group + tid]);
-      float Ls = 0.f;
-      for (int s = 0; s < nsp; ++s) {
-        const float w = expf(cm[s * group + tid] - M);
-        cw[s * group + tid] = w;
-        Ls = __builtin_fmaf(cl[s * group + tid], w, Ls);
-      }
-      lh[tid] = Ls;
-    }
-    __syncthreads();
-    // 16 slices per memory round trip (clamped loads, weight applied only
-    // to live slices), summed in slice order
+    // One memory round trip per MB slices: each thread loads its element's
+    // partials with the slices' (m, l) and folds them in slice order under
+    // a running max (clamped loads; only live slices count).
     constexpr int MB = 16;
     for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
       const uint32_t h = i / HD, dd = i % HD;
-      float O = 0.f;
+      float M = -INFINITY, L = 0.f, O = 0.f;
       for (int s0 = 0; s0 < nsp; s0 += MB) {
-        float o16[MB];
+        float ov[MB], mv[MB], lv[MB];
 #pragma unroll
         for (int r = 0; r < MB; ++r) {
-          const int s = min(s0 + r, nsp - 1);
-          o16[r] = gld(parts + ((size_t)s * group + h) * pstride + dd);
+          const float* ps = parts + ((size_t)min(s0 + r, nsp - 1) * group + h) * pstride;
+          ov[r] = gld(ps + dd);
+          mv[r] = gld(ps + HD);
+          lv[r] = gld(ps + HD + 1);
         }
+        float Mb = M;
 #pragma unroll
         for (int r = 0; r < MB; ++r)
-          if (s0 + r < nsp) O = __builtin_fmaf(o16[r], cw[(s0 + r) * group + h], O);
+          if (s0 + r < nsp) Mb = fmaxf(Mb, mv[r]);
+        const float a = expf(M - Mb);  // 0 for the first batch (M = -inf)
+        L *= a;
+        O *= a;
+#pragma unroll
+        for (int r = 0; r < MB; ++r)
+          if (s0 + r < nsp) {
+            const float w = expf(mv[r] - Mb);
+            L = __builtin_fmaf(lv[r], w, L);
+            O = __builtin_fmaf(ov[r], w, O);
+          }
+        M = Mb;
       }
-      st_coh(atty + ((size_t)j * group + h) * HD + dd, O / lh[h]);
+      st_coh(atty + ((size_t)j * group + h) * HD + dd, O / L);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
   }
@@ -870,6 +863,9 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UF), UF, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     } else {
+      // two rows per unit: the n = 4096 rows give each of the 2048 waves of
+      // a 256-CU grid one unit (UF chunk-steps per item keep the bytes in
+      // flight per wave up)
       constexpr int RD = 2;
       const MegaX<IQ> X(smem, P.ff, need_l);
       const uint32_t total = P.n / RD;

@@ -540,9 +540,9 @@ const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, in
   constexpr int F = MEGA_MM_F32, M = MEGA_MM_MFMA, D = MEGA_MM_DOT4;
   const void* f = nullptr;
   if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 4, 14, 1, 8, M>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 4, 1, 8, D>(lf, of, un, uf, uo, dpl, mm);
   if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, F>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
+  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 4, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
   if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
   if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
   if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
@@ -604,12 +604,17 @@ int mega_setup(talos_hip_ctx* c) {
     if (fn) c->mega_mode = MEGA_MM_MFMA;
   }
   c->mega_mfma = fn != nullptr;
-  const int un = mv_u(w0.q->mat.nchunk), uf = std::min(mv_u(w0.d->mat.nchunk), 2), uo = mv_u(wout->mat.nchunk);
+  // down rows (two per unit) take up to 4 chunk-steps per item for Q4_0 with
+  // int8-plane x, 2 otherwise (Q8_0 has twice the bytes per chunk; f32 x
+  // twice the registers): about 9 KB in flight per wave
+  const int un = mv_u(w0.q->mat.nchunk), uo = mv_u(wout->mat.nchunk);
+  const int ud = mv_u(w0.d->mat.nchunk);
   if (!fn && c->allow_dot4 && (lf == TALOS_FMT_Q4_0 || lf == TALOS_FMT_Q8_0)) {
-    fn = mega_kernel_for(lf, wout->mat.fmt, un, uf, uo, (int)(c->hd / 16), MEGA_MM_DOT4);
+    fn = mega_kernel_for(lf, wout->mat.fmt, un, std::min(ud, lf == TALOS_FMT_Q4_0 ? 4 : 2), uo, (int)(c->hd / 16),
+                         MEGA_MM_DOT4);
     if (fn) c->mega_mode = MEGA_MM_DOT4;
   }
-  if (!fn) fn = mega_kernel_for(lf, wout->mat.fmt, un, uf, uo, (int)(c->hd / 16), MEGA_MM_F32);
+  if (!fn) fn = mega_kernel_for(lf, wout->mat.fmt, un, std::min(ud, 2), uo, (int)(c->hd / 16), MEGA_MM_F32);
   if (!fn) {
     c->mega_ready = true;
     return TALOS_OK;
@@ -626,7 +631,7 @@ int mega_setup(talos_hip_ctx* c) {
   // LDS: x staging for the widest input, or the attention scratch.
   const size_t st = stage_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), 3);
   const uint32_t msplit = mega_attn_max_splits(cf.n_head_kv, (uint32_t)prop.multiProcessorCount);
-  const size_t at = mega_attn_lds_floats(c->hd, c->group, msplit) * 4;
+  const size_t at = mega_attn_lds_floats(c->hd, c->group) * 4;
   c->mega_lds = std::max(st, at);
   if (c->mega_mode != MEGA_MM_F32)
     c->mega_lds = std::max(c->mega_lds, xq_lds_bytes((int)std::max(cf.n_embd, cf.n_ff), MEGA_GPB, MEGA_NW));
