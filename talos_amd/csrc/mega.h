@@ -51,6 +51,7 @@ struct MegaParams {
   int32_t* tokens;
   uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
   uint32_t nsplit, max_chunk;
+  int attn_direct;  // sequences up to this length: one attention item per q head
   int embed;   // 1: x = embedding row of the state token, looked up on the device
   int hidden_only;
   int argmax;  // 0: none, 1: argmax into state, 2: + greedy advance, 3: + feed advance (advance_state)
@@ -299,6 +300,9 @@ __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t
 // partials are written once per launch (coherent stores) and read after the
 // barrier or the slice counter that follows the write.  With nsp > 1 slices
 // the last block to finish for head j merges them in slice order.
+// Short sequences (seq <= P.attn_direct) instead run one item per q head
+// over all positions (ng = 1, nsp = 1): no slice merge, and the group's K/V
+// rows, read by the group's items on one XCD, come from its L2.
 #define MEGA_ATTN_SUB 64
 
 static inline __host__ __device__ uint32_t mega_attn_ppr(uint32_t hd) { return MEGA_NT / (hd / 4); }
@@ -318,8 +322,8 @@ static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group) {
 
 template <int DPL>
 __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float* kc, const float* vc, const float* qv,
-                                               float* atty, float* part, uint32_t j, int split, int nsp, int chunk, int pos,
-                                               float* smem, int tls) {
+                                               float* atty, float* part, uint32_t j, uint32_t hq0, uint32_t ng,
+                                               int split, int nsp, int chunk, int pos, float* smem, int tls) {
 #define ATTN_MARK(k)                  \
   do {                                \
     if (tls >= 0) MEGA_MARK(P, tls + (k)); \
@@ -329,7 +333,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
   constexpr int PPR = MEGA_NT / TPP;      // V positions per round
   constexpr int VR = (MEGA_ATTN_SUB + PPR - 1) / PPR;
   constexpr int KR = MEGA_ATTN_SUB / 32;  // K rounds of 32 positions
-  const uint32_t group = P.group;
+  const uint32_t group = ng;  // the q heads hq0..hq0+ng-1 of this item (all of KV head j's when nsp > 1)
   float* qs = smem;                                  // [group][HD]
   float* sc = qs + group * HD;                       // [group][SUB]
   float* ored = sc + group * MEGA_ATTN_SUB;          // [PPR][group][HD]
@@ -458,7 +462,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
   f4 vA[VR], vB[VR];
   load(kA, vA, 0);
   // q for the group's heads
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)j * group * HD + i);
+  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)hq0 * HD + i);
   __syncthreads();
   ATTN_MARK(0);
   for (int c = 0; c < nsub; c += 2) {
@@ -482,7 +486,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
       const uint32_t h = i / HD, dd = i % HD;
       float o = 0.f;
       for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
-      st_coh(atty + ((size_t)j * group + h) * HD + dd, o / lh[h]);
+      st_coh(atty + ((size_t)hq0 + h) * HD + dd, o / lh[h]);
     }
     __syncthreads();
     ATTN_MARK(4);
@@ -543,7 +547,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
           }
         M = Mb;
       }
-      st_coh(atty + ((size_t)j * group + h) * HD + dd, O / L);
+      st_coh(atty + ((size_t)hq0 + h) * HD + dd, O / L);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
   }
@@ -725,13 +729,23 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       const int seq = pos + 1;
       const int chunk = mega_attn_chunk(seq, P.n_kv, nb);
       const int nsp = (seq + chunk - 1) / chunk;
-      if (nsp > (int)P.nsplit) {
+      if (seq <= P.attn_direct) {
+        // item b: q head (b % n_kv) * group + b / n_kv of KV head b % n_kv,
+        // so a group's items sit on blocks congruent mod n_kv
+        const uint32_t nh = P.n_kv * P.group;
+        for (uint32_t it = blockIdx.x; it < nh; it += nb) {
+          const uint32_t jj = it % P.n_kv, hq = jj * P.group + it / P.n_kv;
+          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, nullptr, jj, hq, 1, 0, 1, seq, pos, smem,
+                              it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
+        }
+      } else if (nsp > (int)P.nsplit) {
         if (threadIdx.x == 0) st_coh_u(G.err, 1u);  // host sized the partials too small
       } else {
         const uint32_t items = P.n_kv * (uint32_t)nsp;
         float* part = P.part + (size_t)l * P.pstride;
         for (uint32_t it = blockIdx.x; it < items; it += nb)
-          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, part, it % P.n_kv, (int)(it / P.n_kv), nsp, chunk, pos, smem,
+          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, part, it % P.n_kv, (it % P.n_kv) * P.group, P.group,
+                              (int)(it / P.n_kv), nsp, chunk, pos, smem,
                               it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
       }
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);

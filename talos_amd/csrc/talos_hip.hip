@@ -108,6 +108,9 @@ struct talos_hip_ctx {
   // TALOS_HIP_DOT4=0 keeps x in f32 for the Q4_0 / Q8_0 layer matvecs of the
   // persistent kernel instead of int8 planes with v_dot4 (the default).
   bool allow_dot4 = true;
+  // TALOS_HIP_ATTN_DIRECT: longest sequence whose attention runs one item
+  // per q head with no slice merge (0: always slices).
+  int attn_direct = 256;
   int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
   MegaParams mp{};
 };
@@ -690,6 +693,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.sync = c->d_sync;
   P.nsplit = msplit;
   P.max_chunk = MEGA_ATTN_SUB;
+  P.attn_direct = c->attn_direct;
   c->mega_fn = fn;
   c->mega_ready = true;
   return TALOS_OK;
@@ -776,6 +780,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_mfma = env && env[0] == '1';
   env = getenv("TALOS_HIP_DOT4");
   c->allow_dot4 = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_ATTN_DIRECT");
+  if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
   c->kv_dim = f.n_head_kv * hd;
   c->group = f.n_head / f.n_head_kv;

@@ -184,9 +184,11 @@ def test_mistral7b_q4_matrix_core_parity(talos, oracle, monkeypatch):
 
 def test_gqa_q8_f32_x_parity(talos, oracle, monkeypatch):
     """The vector-ALU layer matvecs with f32 x (TALOS_HIP_DOT4=0, read when
-    the backend context is created) instead of the default int8-plane x."""
+    the backend context is created) instead of the default int8-plane x, and
+    split-sequence attention at every length (TALOS_HIP_ATTN_DIRECT=0)."""
     from talos_amd import configs
     monkeypatch.setenv("TALOS_HIP_DOT4", "0")
+    monkeypatch.setenv("TALOS_HIP_ATTN_DIRECT", "0")
     wl = configs.gqa_q8()
     _step("gqa_q8 with f32 x: 16-token prompt + 32 greedy steps")
     m = talos.Model.synth(wl.spec)
