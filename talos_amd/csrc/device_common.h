@@ -121,3 +121,29 @@ __device__ __forceinline__ float dot_ub4(uint32_t q, f4 x, float acc) {
   acc = __builtin_fmaf(ub3(q), x.w, acc);
   return acc;
 }
+
+// A staging source loaded as Src::kParts raw float4 (Src::part) and summed
+// (Src::sum) after every load of the stage is issued; kParts == 0: the
+// source's operator() yields the value directly.
+template <class Src>
+struct SrcRaw {
+  f4 p[Src::kParts > 0 ? Src::kParts : 1];
+};
+template <class Src>
+__device__ __forceinline__ SrcRaw<Src> src_load(const Src& s, int e) {
+  SrcRaw<Src> r;
+  if constexpr (Src::kParts > 0) {
+#pragma unroll
+    for (int k = 0; k < Src::kParts; ++k) r.p[k] = s.part(k, e);
+  } else {
+    r.p[0] = s(e);
+  }
+  return r;
+}
+template <class Src>
+__device__ __forceinline__ f4 src_sum(const SrcRaw<Src>& r) {
+  if constexpr (Src::kParts > 1)
+    return Src::sum(r.p);
+  else
+    return r.p[0];
+}

@@ -136,12 +136,14 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
   const int nr = n >> 2;  // real float4 groups
   f4 v[MEGA_VPT];
   // Loads are unconditional (index clamped) so they issue as one batch;
-  // out-of-range groups are zeroed afterwards.
+  // out-of-range groups are zeroed afterwards.  The summands of x are added
+  // only after every load (norm weights included) is out.
   f4 wv[MEGA_VPT];
+  SrcRaw<Src> raw[MEGA_VPT];
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i) {
     const int e4 = i * MEGA_NT + tid;
-    v[i] = src((e4 < nr ? e4 : nr - 1) * 4);
+    raw[i] = src_load(src, (e4 < nr ? e4 : nr - 1) * 4);
   }
   if (norm) {
 #pragma unroll
@@ -153,6 +155,8 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
   __builtin_amdgcn_sched_barrier(0);
   after();
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < MEGA_VPT; ++i) v[i] = src_sum<Src>(raw[i]);
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i)
     if (i * MEGA_NT + tid >= nr) v[i] = f4{0.f, 0.f, 0.f, 0.f};
@@ -257,26 +261,34 @@ struct MegaX<true> {
 // x[e..e+3] of one array, of a + b, or of (a + b) + c: the residual stream
 // is kept as the layer's base plus the o-projection and down-projection
 // outputs, summed in the order of src/model/llama.rs:159-161, 174-176.
+// A source is loaded as kParts raw float4 (part) and summed (sum) once all
+// loads of the stage are out; kParts == 0: operator() yields the value.
 struct Src1 {
+  static constexpr int kParts = 1;
   const float* a;
-  __device__ __forceinline__ f4 operator()(int e) const { return gld4(a + e); }
+  __device__ __forceinline__ f4 part(int, int e) const { return gld4(a + e); }
+  __device__ __forceinline__ static f4 sum(const f4* p) { return p[0]; }
 };
 struct Src2 {
+  static constexpr int kParts = 2;
   const float *a, *b;
-  __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = gld4(a + e), y = gld4(b + e);
-    return f4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+  __device__ __forceinline__ f4 part(int s, int e) const { return gld4((s == 0 ? a : b) + e); }
+  __device__ __forceinline__ static f4 sum(const f4* p) {
+    return f4{p[0].x + p[1].x, p[0].y + p[1].y, p[0].z + p[1].z, p[0].w + p[1].w};
   }
 };
 struct Src3 {
+  static constexpr int kParts = 3;
   const float *a, *b, *c;
-  __device__ __forceinline__ f4 operator()(int e) const {
-    const f4 x = gld4(a + e), y = gld4(b + e), z = gld4(c + e);
-    return f4{(x.x + y.x) + z.x, (x.y + y.y) + z.y, (x.z + y.z) + z.z, (x.w + y.w) + z.w};
+  __device__ __forceinline__ f4 part(int s, int e) const { return gld4((s == 0 ? a : (s == 1 ? b : c)) + e); }
+  __device__ __forceinline__ static f4 sum(const f4* p) {
+    return f4{(p[0].x + p[1].x) + p[2].x, (p[0].y + p[1].y) + p[2].y, (p[0].z + p[1].z) + p[2].z,
+              (p[0].w + p[1].w) + p[2].w};
   }
 };
 
 struct EmbSrc {
+  static constexpr int kParts = 0;
   DevMat M;
   uint32_t tok;
   __device__ __forceinline__ f4 operator()(int e) const {
@@ -716,7 +728,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arr, stage, epi, X.src(LL), lane,
+      mv_stream<LF, RL, UN, false, IQ>(mega_nunits(total, gw, tw), unit, arr, stage, epi, X.src(LL), lane,
                                    pre && l > 0);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
     }
@@ -729,24 +741,21 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       const int seq = pos + 1;
       const int chunk = mega_attn_chunk(seq, P.n_kv, nb);
       const int nsp = (seq + chunk - 1) / chunk;
-      if (seq <= P.attn_direct) {
-        // item b: q head (b % n_kv) * group + b / n_kv of KV head b % n_kv,
-        // so a group's items sit on blocks congruent mod n_kv
-        const uint32_t nh = P.n_kv * P.group;
-        for (uint32_t it = blockIdx.x; it < nh; it += nb) {
-          const uint32_t jj = it % P.n_kv, hq = jj * P.group + it / P.n_kv;
-          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, nullptr, jj, hq, 1, 0, 1, seq, pos, smem,
-                              it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
-        }
-      } else if (nsp > (int)P.nsplit) {
+      // direct: item b is q head (b % n_kv) * group + b / n_kv of KV head
+      // b % n_kv (a group's items sit on blocks congruent mod n_kv), over
+      // all positions; otherwise item b is slice b / n_kv of KV head b % n_kv
+      const bool direct = seq <= P.attn_direct;
+      if (!direct && nsp > (int)P.nsplit) {
         if (threadIdx.x == 0) st_coh_u(G.err, 1u);  // host sized the partials too small
       } else {
-        const uint32_t items = P.n_kv * (uint32_t)nsp;
+        const uint32_t items = direct ? P.n_kv * P.group : P.n_kv * (uint32_t)nsp;
         float* part = P.part + (size_t)l * P.pstride;
-        for (uint32_t it = blockIdx.x; it < items; it += nb)
-          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, part, it % P.n_kv, (it % P.n_kv) * P.group, P.group,
-                              (int)(it / P.n_kv), nsp, chunk, pos, smem,
-                              it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
+        for (uint32_t it = blockIdx.x; it < items; it += nb) {
+          const uint32_t jj = it % P.n_kv, r = it / P.n_kv;
+          mega_attn_item<DPL>(P, LP->kc, LP->vc, q, atty, part, jj, jj * P.group + (direct ? r : 0),
+                              direct ? 1 : P.group, direct ? 0 : (int)r, direct ? 1 : nsp, direct ? seq : chunk, pos,
+                              smem, it == blockIdx.x ? (int)(l * MEGA_TL_PER_LAYER + MEGA_TL_ATTN) : -1);
+        }
       }
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 3);
     }
@@ -795,7 +804,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
 #pragma unroll
         for (int r = 0; r < RL; ++r) st_coh(o_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RL, UN, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+      mv_stream<LF, RL, UN, false, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                    pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     }
@@ -848,7 +857,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, true>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+      mv_stream<LF, RL, UN, true, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                   pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }

@@ -74,12 +74,13 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
   asm volatile("" : "+v"(tid));
   const int n8 = n >> 3;
   f4 v[NR][2], wv[NR][2];
+  SrcRaw<Src> raw[NR][2];  // summed once every load of the stage is out
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int g8 = r * NT + tid;
     const int gg = g8 < n8 ? g8 : n8 - 1;
-    v[r][0] = src(gg * 8);
-    v[r][1] = src(gg * 8 + 4);
+    raw[r][0] = src_load(src, gg * 8);
+    raw[r][1] = src_load(src, gg * 8 + 4);
   }
   if (norm) {
 #pragma unroll
@@ -93,6 +94,11 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
   __builtin_amdgcn_sched_barrier(0);
   after();
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    v[r][0] = src_sum<Src>(raw[r][0]);
+    v[r][1] = src_sum<Src>(raw[r][1]);
+  }
 #pragma unroll
   for (int r = 0; r < NR; ++r)
     if (r * NT + tid >= n8) v[r][0] = v[r][1] = f4{0.f, 0.f, 0.f, 0.f};

@@ -156,70 +156,136 @@ __device__ __forceinline__ int dot4_i8(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// One lane's x for one chunk-step: the chunk's three planes and its
+// (s/254, -off * sum_b).
+struct XIr {
+  u4 pw[3][2];
+  float s254, off;
+};
+
+template <uint32_t FMT>
+__device__ __forceinline__ XIr xi_fetch(const XI& X, int cc) {
+  XIr r;
+  const size_t plane = (size_t)X.nb * 32;
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      r.pw[p][h] = *reinterpret_cast<const u4*>(X.pl + p * plane + ((size_t)h * X.nb + cc) * 16);
+  const float2 sx = X.bs[cc];
+  r.s254 = sx.x * (1.0f / 254.0f);
+  r.off = FMT == TALOS_FMT_Q4_0 ? -8.f * sx.y : 0.f;
+  return r;
+}
+
+// acc[i] += row slot i of chunk-step u against x.  Rows go in pairs; each
+// plane's 8 dot4 run as two chains (4 + 4, summed exactly as integers), so
+// 12 independent chains keep the VALU busy.
+template <uint32_t FMT, int R, int U>
+__device__ __forceinline__ void xi_dot(const MvBuf<FMT, R, U>& B, int u, const XIr& x, bool ok, float (&acc)[R]) {
+  static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "int8-plane x is for Q4_0 / Q8_0");
+  constexpr float k254 = 1.0f / 254.0f;
+  constexpr int RP = R >= 2 ? 2 : 1;
+#pragma unroll
+  for (int i0 = 0; i0 < R; i0 += RP) {
+    uint32_t w[RP][8];
+#pragma unroll
+    for (int j = 0; j < RP; ++j) {
+      const int i = i0 + j;
+      if (FMT == TALOS_FMT_Q4_0) {
+        const u4 q = B.q[i][u][0];
+        w[j][0] = q.x & 0x0F0F0F0Fu;
+        w[j][1] = q.y & 0x0F0F0F0Fu;
+        w[j][2] = q.z & 0x0F0F0F0Fu;
+        w[j][3] = q.w & 0x0F0F0F0Fu;
+        w[j][4] = (q.x >> 4) & 0x0F0F0F0Fu;
+        w[j][5] = (q.y >> 4) & 0x0F0F0F0Fu;
+        w[j][6] = (q.z >> 4) & 0x0F0F0F0Fu;
+        w[j][7] = (q.w >> 4) & 0x0F0F0F0Fu;
+      } else {  // the device layout keeps Q8_0 quants biased by 128 (q ^ 0x80)
+        const u4 q0 = B.q[i][u][0], q1 = B.q[i][u][MvT<FMT>::QW - 1];
+        w[j][0] = q0.x ^ 0x80808080u;
+        w[j][1] = q0.y ^ 0x80808080u;
+        w[j][2] = q0.z ^ 0x80808080u;
+        w[j][3] = q0.w ^ 0x80808080u;
+        w[j][4] = q1.x ^ 0x80808080u;
+        w[j][5] = q1.y ^ 0x80808080u;
+        w[j][6] = q1.z ^ 0x80808080u;
+        w[j][7] = q1.w ^ 0x80808080u;
+      }
+    }
+    int lo[RP][3], hi[RP][3];
+#pragma unroll
+    for (int j = 0; j < RP; ++j)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        lo[j][p] = dot4_i8(w[j][0], x.pw[p][0].x, 0);
+        hi[j][p] = dot4_i8(w[j][4], x.pw[p][1].x, 0);
+      }
+#pragma unroll
+    for (int j = 0; j < RP; ++j)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        lo[j][p] = dot4_i8(w[j][1], x.pw[p][0].y, lo[j][p]);
+        hi[j][p] = dot4_i8(w[j][5], x.pw[p][1].y, hi[j][p]);
+      }
+#pragma unroll
+    for (int j = 0; j < RP; ++j)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        lo[j][p] = dot4_i8(w[j][2], x.pw[p][0].z, lo[j][p]);
+        hi[j][p] = dot4_i8(w[j][6], x.pw[p][1].z, hi[j][p]);
+      }
+#pragma unroll
+    for (int j = 0; j < RP; ++j)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        lo[j][p] = dot4_i8(w[j][3], x.pw[p][0].w, lo[j][p]);
+        hi[j][p] = dot4_i8(w[j][7], x.pw[p][1].w, hi[j][p]);
+      }
+#pragma unroll
+    for (int j = 0; j < RP; ++j) {
+      const int i = i0 + j;
+      const int a = lo[j][0] + hi[j][0], b = lo[j][1] + hi[j][1], c = lo[j][2] + hi[j][2];
+      // |a| <= 32 * 128 * 127, so 254 * a + b fits an int32
+      const float t = __builtin_fmaf((float)c, k254, (float)(a * 254 + b));
+      const float d = ok ? f16_to_f32((uint16_t)B.a[i][u]) : 0.f;
+      acc[i] = __builtin_fmaf(d, __builtin_fmaf(x.s254, t, x.off), acc[i]);
+    }
+  }
+}
+
+// x from LDS, the next chunk-step's planes read while this one computes.
 template <uint32_t FMT, int R, int U>
 __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XI& X, int nc, int c0, int lane,
                                            float (&acc)[R]) {
-  static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "int8-plane x is for Q4_0 / Q8_0");
-  constexpr float k254 = 1.0f / 254.0f;
-  const size_t plane = (size_t)X.nb * 32;
+  auto cc = [&](int u) {
+    const int c = c0 + u * TALOS_WAVE + lane;
+    return c < nc ? c : nc - 1;
+  };
+  XIr x = xi_fetch<FMT>(X, cc(0));
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int c = c0 + u * TALOS_WAVE + lane;
-    const bool ok = c < nc;
-    const int cc = ok ? c : nc - 1;
-    u4 pw[3][2];
-#pragma unroll
-    for (int p = 0; p < 3; ++p)
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        pw[p][h] = *reinterpret_cast<const u4*>(X.pl + p * plane + ((size_t)h * X.nb + cc) * 16);
-    const float2 sx = X.bs[cc];
-    const float s254 = sx.x * k254;
-    const float off = FMT == TALOS_FMT_Q4_0 ? -8.f * sx.y : 0.f;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      uint32_t w[8];
-      if (FMT == TALOS_FMT_Q4_0) {
-        const u4 q = B.q[i][u][0];
-        w[0] = q.x & 0x0F0F0F0Fu;
-        w[1] = q.y & 0x0F0F0F0Fu;
-        w[2] = q.z & 0x0F0F0F0Fu;
-        w[3] = q.w & 0x0F0F0F0Fu;
-        w[4] = (q.x >> 4) & 0x0F0F0F0Fu;
-        w[5] = (q.y >> 4) & 0x0F0F0F0Fu;
-        w[6] = (q.z >> 4) & 0x0F0F0F0Fu;
-        w[7] = (q.w >> 4) & 0x0F0F0F0Fu;
-      } else {  // the device layout keeps Q8_0 quants biased by 128 (q ^ 0x80)
-        const u4 q0 = B.q[i][u][0], q1 = B.q[i][u][MvT<FMT>::QW - 1];
-        w[0] = q0.x ^ 0x80808080u;
-        w[1] = q0.y ^ 0x80808080u;
-        w[2] = q0.z ^ 0x80808080u;
-        w[3] = q0.w ^ 0x80808080u;
-        w[4] = q1.x ^ 0x80808080u;
-        w[5] = q1.y ^ 0x80808080u;
-        w[6] = q1.z ^ 0x80808080u;
-        w[7] = q1.w ^ 0x80808080u;
-      }
-      int dp[3];
-#pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        int a = 0;
-        a = dot4_i8(w[0], pw[p][0].x, a);
-        a = dot4_i8(w[1], pw[p][0].y, a);
-        a = dot4_i8(w[2], pw[p][0].z, a);
-        a = dot4_i8(w[3], pw[p][0].w, a);
-        a = dot4_i8(w[4], pw[p][1].x, a);
-        a = dot4_i8(w[5], pw[p][1].y, a);
-        a = dot4_i8(w[6], pw[p][1].z, a);
-        a = dot4_i8(w[7], pw[p][1].w, a);
-        dp[p] = a;
-      }
-      // |dp[0]| <= 32 * 128 * 127, so 254 * dp[0] + dp[1] fits an int32
-      const float t = __builtin_fmaf((float)dp[2], k254, (float)(dp[0] * 254 + dp[1]));
-      const float d = ok ? f16_to_f32((uint16_t)B.a[i][u]) : 0.f;
-      acc[i] = __builtin_fmaf(d, __builtin_fmaf(s254, t, off), acc[i]);
-    }
+    XIr xn;
+    if (u + 1 < U) xn = xi_fetch<FMT>(X, cc(u + 1));
+    xi_dot<FMT, R, U>(B, u, x, c0 + u * TALOS_WAVE + lane < nc, acc);
+    if (u + 1 < U) x = xn;
   }
+}
+
+// x held in registers for the whole phase (rows that fit one item: every
+// item covers the same chunks, so a lane's x never changes).
+template <int U>
+struct XIreg {
+  XIr x[U];
+  bool ok[U];
+};
+
+template <uint32_t FMT, int R, int U>
+__device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XIreg<U>& X, int, int, int,
+                                           float (&acc)[R]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) xi_dot<FMT, R, U>(B, u, X.x[u], X.ok[u], acc);
 }
 
 // Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
@@ -227,7 +293,16 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XI& 
 // them).  `arrive()` and `stage(pf)` are called once by every thread of the
 // block; `stage` calls pf() once, at the point where the first item's weight
 // loads should be issued.  Without `pre` they are issued after `stage`.
-template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class ArriveFn, class StageFn, class EpiFn, class XS>
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class EpiFn, class XS>
+__device__ __forceinline__ void mv_run(int nitems, int iters, int nc, UnitFn& unit, EpiFn& epi, const XS& xs, int lane,
+                                       MvBuf<FMT, R, U>& b0, MvBuf<FMT, R, U>& b1, const DevMat& A0, const DevMat& A1,
+                                       uint32_t r0, uint32_t rmax);
+
+// XREG (int8-plane x only): the caller guarantees a row fits one item
+// (nchunk <= U * 64), so a lane's x is the same for every item and is read
+// from LDS once, into registers.
+template <uint32_t FMT, int R, int U, bool PAIR, bool XREG = false, class UnitFn, class ArriveFn, class StageFn,
+          class EpiFn, class XS>
 __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
                                           const XS& xs, int lane, bool pre) {
   // Every weight load below is issued unconditionally (an idle wave's first
@@ -254,6 +329,25 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arri
     pf();
   }
   const int nitems = nunits > 0 ? nunits * iters : 0;
+  if constexpr (XREG) {
+    XIreg<U> xr;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = u * TALOS_WAVE + lane;
+      xr.ok[u] = c < nc;
+      xr.x[u] = xi_fetch<FMT>(xs, c < nc ? c : nc - 1);
+    }
+    mv_run<FMT, R, U, PAIR>(nitems, 1, nc, unit, epi, xr, lane, b0, b1, A0, A1, r0, rmax);
+  } else {
+    mv_run<FMT, R, U, PAIR>(nitems, iters, nc, unit, epi, xs, lane, b0, b1, A0, A1, r0, rmax);
+  }
+}
+
+// The item loop of mv_stream (item 0 already issued into b0).
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class EpiFn, class XS>
+__device__ __forceinline__ void mv_run(int nitems, int iters, int nc, UnitFn& unit, EpiFn& epi, const XS& xs, int lane,
+                                       MvBuf<FMT, R, U>& b0, MvBuf<FMT, R, U>& b1, const DevMat& A0, const DevMat& A1,
+                                       uint32_t r0, uint32_t rmax) {
   float acc[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) acc[i] = 0.f;

@@ -612,7 +612,10 @@ int mega_setup(talos_hip_ctx* c) {
   // twice the registers): about 9 KB in flight per wave
   const int un = mv_u(w0.q->mat.nchunk), uo = mv_u(wout->mat.nchunk);
   const int ud = mv_u(w0.d->mat.nchunk);
-  if (!fn && c->allow_dot4 && (lf == TALOS_FMT_Q4_0 || lf == TALOS_FMT_Q8_0)) {
+  // (int8-plane x also keeps each lane's x of an n-wide row in registers,
+  // so such a row must fit one item: n / 32 <= un * 64)
+  if (!fn && c->allow_dot4 && (lf == TALOS_FMT_Q4_0 || lf == TALOS_FMT_Q8_0) &&
+      cf.n_embd / 32 <= (uint32_t)un * 64) {
     fn = mega_kernel_for(lf, wout->mat.fmt, un, std::min(ud, lf == TALOS_FMT_Q4_0 ? 4 : 2), uo, (int)(c->hd / 16),
                          MEGA_MM_DOT4);
     if (fn) c->mega_mode = MEGA_MM_DOT4;
