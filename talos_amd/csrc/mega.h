@@ -783,12 +783,15 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UN), UN, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     } else {
+      // with x in registers, two rows per unit: the n rows spread over every
+      // wave of the grid (4096 rows, 2048 waves)
+      constexpr int RP = IQ ? 2 : RL;
       const MegaX<IQ> X(smem, P.n, need_l);
-      const uint32_t total = P.n / RL;
+      const uint32_t total = P.n / RP;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
         A0 = const_mat(&LP->o);
         A1 = A0;
-        r0 = (gw + (uint32_t)k * tw) * RL;
+        r0 = (gw + (uint32_t)k * tw) * RP;
         rmax = LP->o.rows;
       };
       auto stage = [&](auto&& pf) {
@@ -798,13 +801,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         X.stage(src, P.n, nullptr, 0.f, false, nullptr, 0, 0, pf);
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
-      auto epi = [&](int k, const float(&y)[RL]) {
+      auto epi = [&](int k, const float(&y)[RP]) {
         if (lane != 0) return;
-        const uint32_t r0 = (gw + (uint32_t)k * tw) * RL;
+        const uint32_t r0 = (gw + (uint32_t)k * tw) * RP;
 #pragma unroll
-        for (int r = 0; r < RL; ++r) st_coh(o_out + r0 + r, y[r]);
+        for (int r = 0; r < RP; ++r) st_coh(o_out + r0 + r, y[r]);
       };
-      mv_stream<LF, RL, UN, false, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+      mv_stream<LF, RP, UN, false, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                    pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 5);
     }
