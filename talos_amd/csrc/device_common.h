@@ -129,16 +129,24 @@ template <class Src>
 struct SrcRaw {
   f4 p[Src::kParts > 0 ? Src::kParts : 1];
 };
+// Parts [0, Src::kEarly) are final before the grid barrier that precedes
+// the stage and may be loaded ahead of it (src_load_early); the rest after
+// it (src_load_late).
 template <class Src>
-__device__ __forceinline__ SrcRaw<Src> src_load(const Src& s, int e) {
-  SrcRaw<Src> r;
+__device__ __forceinline__ void src_load_early(const Src& s, int e, SrcRaw<Src>& r) {
   if constexpr (Src::kParts > 0) {
 #pragma unroll
-    for (int k = 0; k < Src::kParts; ++k) r.p[k] = s.part(k, e);
+    for (int k = 0; k < Src::kEarly; ++k) r.p[k] = s.part(k, e);
+  }
+}
+template <class Src>
+__device__ __forceinline__ void src_load_late(const Src& s, int e, SrcRaw<Src>& r) {
+  if constexpr (Src::kParts > 0) {
+#pragma unroll
+    for (int k = Src::kEarly; k < Src::kParts; ++k) r.p[k] = s.part(k, e);
   } else {
     r.p[0] = s(e);
   }
-  return r;
 }
 template <class Src>
 __device__ __forceinline__ f4 src_sum(const SrcRaw<Src>& r) {

@@ -121,10 +121,10 @@ static inline size_t mega_sync_words(uint32_t nblocks) { return (size_t)nblocks 
 #define MEGA_VPT 8
 #define MEGA_STAGE_MAX (MEGA_VPT * MEGA_NT * 4)
 
-template <int MEGA_VPT_N, class Src, class After>
+template <int MEGA_VPT_N, class Src, class After, class Wait>
 __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __restrict__ w, float eps, bool norm,
                                              const XStage& X, int need, float* pub, int pub_lo, int pub_hi,
-                                             After after) {
+                                             After after, Wait wait) {
 #undef MEGA_VPT
 #define MEGA_VPT MEGA_VPT_N
   // Opaque copy of the thread index: keeps the compiler from hoisting this
@@ -143,7 +143,7 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i) {
     const int e4 = i * MEGA_NT + tid;
-    raw[i] = src_load(src, (e4 < nr ? e4 : nr - 1) * 4);
+    src_load_early(src, (e4 < nr ? e4 : nr - 1) * 4, raw[i]);
   }
   if (norm) {
 #pragma unroll
@@ -151,6 +151,14 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
       const int e4 = i * MEGA_NT + tid;
       wv[i] = gld4(w + (e4 < nr ? e4 : nr - 1) * 4);
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < MEGA_VPT; ++i) {
+    const int e4 = i * MEGA_NT + tid;
+    src_load_late(src, (e4 < nr ? e4 : nr - 1) * 4, raw[i]);
   }
   __builtin_amdgcn_sched_barrier(0);
   after();
@@ -193,30 +201,30 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
 #define MEGA_VPT 8
 }
 
-template <class Src, class After>
+template <class Src, class After, class Wait>
 __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restrict__ w, float eps, bool norm,
                                            const XStage& X, int need, float* pub, int pub_lo, int pub_hi,
-                                           After after) {
+                                           After after, Wait wait) {
   if (n <= 2 * MEGA_NT * 4)
-    mega_stage_v<2>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after);
+    mega_stage_v<2>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after, wait);
   else
-    mega_stage_v<MEGA_VPT>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after);
+    mega_stage_v<MEGA_VPT>(src, n, w, eps, norm, X, need, pub, pub_lo, pub_hi, after, wait);
 }
 
 // Groups per block the matrix-core phases may need (LDS partial sums).
 #define MEGA_GPB 8
 
 // stage_xq with the fewest rounds of 8 elements per thread covering n.
-template <class Src, class After>
+template <class Src, class After, class Wait>
 __device__ __forceinline__ void stage_xq_n(Src src, int n, const float* w, float eps, bool norm, const XQ& X,
-                                           float* pub, int pub_lo, int pub_hi, After after) {
+                                           float* pub, int pub_lo, int pub_hi, After after, Wait wait) {
   const int n8 = n >> 3;
   if (n8 <= MEGA_NT)
-    stage_xq<1, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
+    stage_xq<1, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after, wait);
   else if (n8 <= 2 * MEGA_NT)
-    stage_xq<2, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
+    stage_xq<2, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after, wait);
   else
-    stage_xq<4, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after);
+    stage_xq<4, MEGA_NT>(src, n, w, eps, norm, X, pub, pub_lo, pub_hi, after, wait);
 }
 
 // Matvec modes of the persistent kernel: f32 x on the vector ALUs, Q4_0 on
@@ -231,10 +239,10 @@ struct MegaX {
   XStage X;
   int need;
   __device__ __forceinline__ MegaX(float* smem, int n, int need_) : X(carve_x(smem, n, need_)), need(need_) {}
-  template <class Src, class After>
+  template <class Src, class After, class Wait>
   __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
-                                        int hi, After after) const {
-    mega_stage(src, n, w, eps, norm, X, need, pub, lo, hi, after);
+                                        int hi, After after, Wait wait) const {
+    mega_stage(src, n, w, eps, norm, X, need, pub, lo, hi, after, wait);
   }
   __device__ __forceinline__ XF src(int layout) const { return XF{X.xs[layout], X.xsum}; }
 };
@@ -242,16 +250,16 @@ template <>
 struct MegaX<true> {
   XQ X;
   __device__ __forceinline__ MegaX(float* smem, int n, int) : X(carve_xq(smem, n, MEGA_GPB, MEGA_NW)) {}
-  template <class Src, class After>
+  template <class Src, class After, class Wait>
   __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
-                                        int hi, After after) const {
+                                        int hi, After after, Wait wait) const {
     const int n8 = n >> 3;
     if (n8 <= MEGA_NT)
-      stage_xq<1, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+      stage_xq<1, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
     else if (n8 <= 2 * MEGA_NT)
-      stage_xq<2, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+      stage_xq<2, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
     else
-      stage_xq<4, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after);
+      stage_xq<4, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
   }
   __device__ __forceinline__ XI src(int) const {
     return XI{reinterpret_cast<const uint8_t*>(X.pl), X.bs, X.nb};
@@ -264,21 +272,21 @@ struct MegaX<true> {
 // A source is loaded as kParts raw float4 (part) and summed (sum) once all
 // loads of the stage are out; kParts == 0: operator() yields the value.
 struct Src1 {
-  static constexpr int kParts = 1;
+  static constexpr int kParts = 1, kEarly = 0;
   const float* a;
   __device__ __forceinline__ f4 part(int, int e) const { return gld4(a + e); }
   __device__ __forceinline__ static f4 sum(const f4* p) { return p[0]; }
 };
-struct Src2 {
-  static constexpr int kParts = 2;
+struct Src2 {  // the layer's residual base (final early) + the o-projection
+  static constexpr int kParts = 2, kEarly = 1;
   const float *a, *b;
   __device__ __forceinline__ f4 part(int s, int e) const { return gld4((s == 0 ? a : b) + e); }
   __device__ __forceinline__ static f4 sum(const f4* p) {
     return f4{p[0].x + p[1].x, p[0].y + p[1].y, p[0].z + p[1].z, p[0].w + p[1].w};
   }
 };
-struct Src3 {
-  static constexpr int kParts = 3;
+struct Src3 {  // base and o-projection (final early) + the down-projection
+  static constexpr int kParts = 3, kEarly = 2;
   const float *a, *b, *c;
   __device__ __forceinline__ f4 part(int s, int e) const { return gld4((s == 0 ? a : (s == 1 ? b : c)) + e); }
   __device__ __forceinline__ static f4 sum(const f4* p) {
@@ -288,7 +296,7 @@ struct Src3 {
 };
 
 struct EmbSrc {
-  static constexpr int kParts = 0;
+  static constexpr int kParts = 0, kEarly = 0;
   DevMat M;
   uint32_t tok;
   __device__ __forceinline__ f4 operator()(int e) const {
@@ -635,17 +643,18 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       };
       auto stage = [&](auto&& pf) {
         if (l > 0) {
-          wait();
-          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
           // x = (base + attproj) + down of the previous layer; publish it
           Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf);
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf, [&] {
+            wait();
+            MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
+          });
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf);
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, base, pub_lo, pub_hi, pf, [] {});
         } else {
           Src1 src{P.x};
-          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, nullptr, 0, 0, pf);
+          stage_xq_n(src, P.n, LP->attn_norm, P.eps, true, X, nullptr, 0, 0, pf, [] {});
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -689,17 +698,18 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       };
       auto stage = [&](auto&& pf) {
         if (l > 0) {
-          wait();
-          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
           // x = (base + attproj) + down of the previous layer; publish it
           Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [&] {
+            wait();
+            MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
+          });
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [] {});
         } else {
           Src1 src{P.x};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, nullptr, 0, 0, pf);
+          X.stage(src, P.n, LP->attn_norm, P.eps, true, nullptr, 0, 0, pf, [] {});
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -769,10 +779,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         row0 = (uint32_t)gi * 16;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
         Src1 src{atty};
-        stage_xq_n(src, P.n, nullptr, 0.f, false, X, nullptr, 0, 0, pf);
+        stage_xq_n(src, P.n, nullptr, 0.f, false, X, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
       auto fin = [&](int gi, int jj, float y0, float y1) {
@@ -795,10 +806,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = LP->o.rows;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
         Src1 src{atty};
-        X.stage(src, P.n, nullptr, 0.f, false, nullptr, 0, 0, pf);
+        X.stage(src, P.n, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
       };
       auto epi = [&](int k, const float(&y)[RP]) {
@@ -821,10 +833,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         row0 = (uint32_t)gi * 8;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
         Src2 src{base, o_out};
-        stage_xq_n(src, P.n, LP->ffn_norm, P.eps, true, X, nullptr, 0, 0, pf);
+        stage_xq_n(src, P.n, LP->ffn_norm, P.eps, true, X, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto fin = [&](int gi, int jj, float g, float u) {
@@ -843,10 +856,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = LP->g.rows;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
         Src2 src{base, o_out};
-        X.stage(src, P.n, LP->ffn_norm, P.eps, true, nullptr, 0, 0, pf);
+        X.stage(src, P.n, LP->ffn_norm, P.eps, true, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto epi = [&](int k, const float(&y)[RL]) {
@@ -875,10 +889,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         row0 = (uint32_t)gi * 16;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
         Src1 src{h};
-        stage_xq_n(src, P.ff, nullptr, 0.f, false, X, nullptr, 0, 0, pf);
+        stage_xq_n(src, P.ff, nullptr, 0.f, false, X, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
       };
       auto fin = [&](int gi, int jj, float y0, float y1) {
@@ -902,10 +917,11 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         rmax = LP->d.rows;
       };
       auto stage = [&](auto&& pf) {
-        wait();
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
         Src1 src{h};
-        X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf);
+        X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
+          wait();
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+        });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
       };
       auto epi = [&](int k, const float(&y)[RD]) {
@@ -953,9 +969,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       rmax = P.out_w.rows;
     };
     auto stage = [&](auto&& pf) {
-      wait();
       Src3 src{last, last_o, last_d};
-      X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf);
+      X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
       MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
     };
     auto epi = [&](int k, const float(&y)[RO]) {

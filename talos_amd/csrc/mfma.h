@@ -61,15 +61,17 @@ __device__ __forceinline__ float rne(float t) { return __builtin_rintf(t); }
 
 // Stage x (n floats, n % 32 == 0, n <= NR*512*8) as int8 planes, optionally
 // as rmsnorm(x)*w (src/math/ops.rs:5-12).  Thread t owns 8 consecutive
-// elements per round (4 threads = one block).  All loads are issued first,
-// then after() (the matvec's first weight loads), then the arithmetic.  The
-// block publishes its raw x slice [pub_lo, pub_hi) to `pub` (coherent).
+// elements per round (4 threads = one block).  The loads of the parts of x
+// that are final before the barrier (and of w) are issued first, then
+// wait() (the barrier), then the other loads, then after() (the matvec's
+// first weight loads), then the arithmetic.  The block publishes its raw x
+// slice [pub_lo, pub_hi) to `pub` (coherent).
 // Plane layout: [3][nb][32] bytes, or with SPLIT [3][2][nb] 16-byte words
 // (word h of block b at (h * nb + b) * 16: a wave reading one block per lane
 // touches consecutive words, free of LDS bank conflicts).
-template <int NR, int NT, bool SPLIT = false, class Src, class After>
+template <int NR, int NT, bool SPLIT = false, class Src, class After, class Wait>
 __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict__ w, float eps, bool norm,
-                                         const XQ& X, float* pub, int pub_lo, int pub_hi, After after) {
+                                         const XQ& X, float* pub, int pub_lo, int pub_hi, After after, Wait wait) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int n8 = n >> 3;
@@ -79,8 +81,8 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
   for (int r = 0; r < NR; ++r) {
     const int g8 = r * NT + tid;
     const int gg = g8 < n8 ? g8 : n8 - 1;
-    raw[r][0] = src_load(src, gg * 8);
-    raw[r][1] = src_load(src, gg * 8 + 4);
+    src_load_early(src, gg * 8, raw[r][0]);
+    src_load_early(src, gg * 8 + 4, raw[r][1]);
   }
   if (norm) {
 #pragma unroll
@@ -90,6 +92,16 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
       wv[r][0] = gld4(w + gg * 8);
       wv[r][1] = gld4(w + gg * 8 + 4);
     }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int g8 = r * NT + tid;
+    const int gg = g8 < n8 ? g8 : n8 - 1;
+    src_load_late(src, gg * 8, raw[r][0]);
+    src_load_late(src, gg * 8 + 4, raw[r][1]);
   }
   __builtin_amdgcn_sched_barrier(0);
   after();
