@@ -846,8 +846,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UN * MEGA_NW), UN * MEGA_NW, 1, true, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     } else {
+      // with x in registers, one row pair per unit: 14336 pairs give each of
+      // the 2048 waves of a 256-CU grid exactly 7
+      constexpr int RG = IQ ? 2 : RL, PR = RG / 2;
       const MegaX<IQ> X(smem, P.n, need_l);
-      constexpr int PR = RL / 2;
       const uint32_t total = (P.ff + PR - 1) / PR;
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
         A0 = const_mat(&LP->g);
@@ -863,7 +865,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
-      auto epi = [&](int k, const float(&y)[RL]) {
+      auto epi = [&](int k, const float(&y)[RG]) {
         if (lane != 0) return;
         const uint32_t p0 = (gw + (uint32_t)k * tw) * PR;
 #pragma unroll
@@ -874,7 +876,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RL, UN, true, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+      mv_stream<LF, RG, UN, true, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
                                   pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
