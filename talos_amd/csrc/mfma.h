@@ -155,21 +155,24 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
     uint32_t pa[2], pb[2], pc[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
+      // t - a is exact, so fma(t, 254, -254 a) is (t - a) * 254 rounded
+      // once; each integer piece goes in as the biased byte piece + 128
+      // (v_cvt_pk_u8_f32 of an exact integer), unbiased by one xor per word.
       uint32_t wa = 0, wb = 0, wc = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float t = x[hh * 4 + k] * inv;
         const float a = rne(t);
-        const float t2 = (t - a) * 254.f;
+        const float t2 = __builtin_fmaf(t, 254.f, -254.f * a);
         const float b = rne(t2);
-        const float c = rne((t2 - b) * 254.f);
-        wa |= ((uint32_t)(int)a & 0xFFu) << (8 * k);
-        wb |= ((uint32_t)(int)b & 0xFFu) << (8 * k);
-        wc |= ((uint32_t)(int)c & 0xFFu) << (8 * k);
+        const float c = rne(__builtin_fmaf(t2, 254.f, -254.f * b));
+        wa = __builtin_amdgcn_cvt_pk_u8_f32(a + 128.f, k, wa);
+        wb = __builtin_amdgcn_cvt_pk_u8_f32(b + 128.f, k, wb);
+        wc = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.f, k, wc);
       }
-      pa[hh] = wa;
-      pb[hh] = wb;
-      pc[hh] = wc;
+      pa[hh] = wa ^ 0x80808080u;
+      pb[hh] = wb ^ 0x80808080u;
+      pc[hh] = wc ^ 0x80808080u;
     }
     if (ok) {
       const int blk = g8 >> 2, off = (g8 & 3) * 8;
