@@ -52,6 +52,7 @@ struct MegaParams {
   uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
   uint32_t nsplit, max_chunk;
   int attn_direct;  // sequences up to this length: one attention item per q head
+  int dsplit;       // down-projection in MEGA_DSPLIT column parts (int8-plane x)
   int embed;   // 1: x = embedding row of the state token, looked up on the device
   int hidden_only;
   int argmax;  // 0: none, 1: argmax into state, 2: + greedy advance, 3: + feed advance (advance_state)
@@ -213,6 +214,10 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
 
 // Groups per block the matrix-core phases may need (LDS partial sums).
 #define MEGA_GPB 8
+// Column parts of the split down-projection and the most rows a team of
+// MEGA_DSPLIT waves may own.
+#define MEGA_DSPLIT 4
+#define MEGA_DSPLIT_ROWS 16
 
 // stage_xq with the fewest rounds of 8 elements per thread covering n.
 template <class Src, class After, class Wait>
@@ -262,7 +267,7 @@ struct MegaX<true> {
       stage_xq<4, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
   }
   __device__ __forceinline__ XI src(int) const {
-    return XI{reinterpret_cast<const uint8_t*>(X.pl), X.bs, X.nb};
+    return XI{reinterpret_cast<const uint8_t*>(X.pl), X.bs, X.nb, 0};
   }
 };
 
@@ -906,34 +911,87 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       mq_phase<mq_item_tiles(UF), UF, MEGA_NW, false, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     } else {
-      // two rows per unit: the n = 4096 rows give each of the 2048 waves of
-      // a 256-CU grid one unit (UF chunk-steps per item keep the bytes in
-      // flight per wave up)
-      constexpr int RD = 2;
-      const MegaX<IQ> X(smem, P.ff, need_l);
-      const uint32_t total = P.n / RD;
-      auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
-        A0 = const_mat(&LP->d);
-        A1 = A0;
-        r0 = (gw + (uint32_t)k * tw) * RD;
-        rmax = LP->d.rows;
-      };
-      auto stage = [&](auto&& pf) {
-        Src1 src{h};
-        X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
-          wait();
-          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
-        });
-        MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
-      };
-      auto epi = [&](int k, const float(&y)[RD]) {
-        if (lane != 0) return;
-        const uint32_t r0 = (gw + (uint32_t)k * tw) * RD;
+      auto whole_rows = [&] {
+        // two rows per unit: the n = 4096 rows give each of the 2048 waves of
+        // a 256-CU grid one unit (UF chunk-steps per item keep the bytes in
+        // flight per wave up)
+        constexpr int RD = 2;
+        const MegaX<IQ> X(smem, P.ff, need_l);
+        const uint32_t total = P.n / RD;
+        auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+          A0 = const_mat(&LP->d);
+          A1 = A0;
+          r0 = (gw + (uint32_t)k * tw) * RD;
+          rmax = LP->d.rows;
+        };
+        auto stage = [&](auto&& pf) {
+          Src1 src{h};
+          X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
+            wait();
+            MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+          });
+          MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
+        };
+        auto epi = [&](int k, const float(&y)[RD]) {
+          if (lane != 0) return;
+          const uint32_t r0 = (gw + (uint32_t)k * tw) * RD;
+  #pragma unroll
+          for (int r = 0; r < RD; ++r) st_coh(d_out + r0 + r, y[r]);
+        };
+        mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+                                     pre);
+            };
+      if constexpr (IQ) {
+        if (P.dsplit) {
+          // The down rows in column quarters: the four waves of a team (waves
+          // 4t..4t+3 of a block) each take one quarter of the columns of the
+          // team's rows, two rows per unit, with the x of their quarter held in
+          // registers; the four quarter sums of a row meet in LDS and are added
+          // in quarter order.
+          constexpr int KS = MEGA_DSPLIT, RD = 2, TEAMS = MEGA_NW / KS;
+          __shared__ float dpart[TEAMS][KS][MEGA_DSPLIT_ROWS];
+          const MegaX<IQ> X(smem, P.ff, need_l);
+          const int part = wave % KS, tm = wave / KS;
+          const uint32_t rpt = P.n / (nb * TEAMS);  // rows per team
+          const uint32_t team = blockIdx.x * TEAMS + tm;
+          const uint32_t qn = LP->d.nchunk / KS;  // chunks per quarter
+          auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+            A0 = const_mat(&LP->d);
+            A0.q += (size_t)part * qn * fmt_chunk_qbytes(LF);
+            A0.d += (size_t)part * qn;
+            A0.nchunk = qn;
+            A1 = A0;
+            r0 = team * rpt + (uint32_t)k * RD;
+            rmax = LP->d.rows;
+          };
+          auto stage = [&](auto&& pf) {
+            Src1 src{h};
+            X.stage(src, P.ff, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
+              wait();
+              MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+            });
+            MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
+          };
+          auto epi = [&](int k, const float(&y)[RD]) {
+            if (lane != 0) return;
 #pragma unroll
-        for (int r = 0; r < RD; ++r) st_coh(d_out + r0 + r, y[r]);
-      };
-      mv_stream<LF, RD, UF, false>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
-                                   pre);
+            for (int r = 0; r < RD; ++r) dpart[tm][part][k * RD + r] = y[r];
+          };
+          XI xq = X.src(LL);
+          xq.c0 = part * (int)qn;
+          mv_stream<LF, RD, UN, false, true>((int)(rpt / RD), unit, arrive, stage, epi, xq, lane, pre);
+          __syncthreads();
+          if (threadIdx.x < TEAMS * rpt) {
+            const uint32_t t = threadIdx.x / rpt, r = threadIdx.x % rpt;
+            const float v = ((dpart[t][0][r] + dpart[t][1][r]) + dpart[t][2][r]) + dpart[t][3][r];
+            st_coh(d_out + (blockIdx.x * TEAMS + t) * rpt + r, v);
+          }
+        } else {
+          whole_rows();
+        }
+      } else {
+        whole_rows();
+      }
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 9);
     }
   }

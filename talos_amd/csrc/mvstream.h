@@ -38,11 +38,14 @@ struct MvBuf {
 // Load one item: rows r0 + slot (clamped to rmax - 1; the caller masks
 // those results), chunks c0 + u*64 + lane (clamped to nchunk - 1, masked in
 // mv_compute).  PAIR interleaves two matrices: slot 2k -> A0 row r0+k,
-// slot 2k+1 -> A1 row r0+k.
+// slot 2k+1 -> A1 row r0+k.  Q4_0/Q8_0 rows are cols / 32 chunks apart, so
+// a view of a column range (q and d advanced to its first chunk, nchunk
+// its length) reads like a whole matrix.
 template <uint32_t FMT, int R, int U, bool PAIR>
 __device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, const DevMat& A1, uint32_t r0,
                                         uint32_t rmax, int c0, int lane) {
   const int nc = (int)A0.nchunk;
+  const int rs = (FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0) ? (int)(A0.cols >> 5) : nc;
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const DevMat& M = (PAIR && (i & 1)) ? A1 : A0;
@@ -52,7 +55,7 @@ __device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, c
     for (int u = 0; u < U; ++u) {
       int c = c0 + u * TALOS_WAVE + lane;
       c = c < nc ? c : nc - 1;
-      const size_t ci = (size_t)row * nc + c;
+      const size_t ci = (size_t)row * rs + c;
       if (FMT == TALOS_FMT_F32) {
         B.q[i][u][0] = ldg4(M.q + ci * 16);
       } else if (FMT == TALOS_FMT_Q4_0) {
@@ -86,6 +89,7 @@ struct XI {
   const uint8_t* pl;
   const float2* bs;
   int nb;
+  int c0;  // chunk c of the matvec reads block c0 + c of x
 };
 
 // acc[i] += <row slot i, x> over this item's chunks.
@@ -166,6 +170,7 @@ struct XIr {
 template <uint32_t FMT>
 __device__ __forceinline__ XIr xi_fetch(const XI& X, int cc) {
   XIr r;
+  cc += X.c0;
   const size_t plane = (size_t)X.nb * 32;
 #pragma unroll
   for (int p = 0; p < 3; ++p)

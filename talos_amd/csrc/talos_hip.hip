@@ -111,6 +111,8 @@ struct talos_hip_ctx {
   // TALOS_HIP_ATTN_DIRECT: longest sequence whose attention runs one item
   // per q head with no slice merge (0: always slices).
   int attn_direct = 256;
+  // TALOS_HIP_DSPLIT=0 keeps the down-projection rows whole.
+  bool allow_dsplit = true;
   int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
   MegaParams mp{};
 };
@@ -697,6 +699,15 @@ int mega_setup(talos_hip_ctx* c) {
   P.nsplit = msplit;
   P.max_chunk = MEGA_ATTN_SUB;
   P.attn_direct = c->attn_direct;
+  {
+    // split down-projection: whole quarters of the row chunks that fit one
+    // item, and an even number of rows per team of MEGA_DSPLIT waves
+    const uint32_t teams = c->mega_blocks * (MEGA_NW / MEGA_DSPLIT), dch = cf.n_ff / 32;
+    const uint32_t rpt = cf.n_embd / teams;
+    P.dsplit = c->mega_mode == MEGA_MM_DOT4 && c->allow_dsplit && dch % MEGA_DSPLIT == 0 &&
+               dch / MEGA_DSPLIT <= (uint32_t)mv_u(cf.n_embd / 32) * 64 && rpt * teams == cf.n_embd &&
+               rpt % 2 == 0 && rpt <= MEGA_DSPLIT_ROWS && rpt * (MEGA_NW / MEGA_DSPLIT) <= MEGA_NT;
+  }
   c->mega_fn = fn;
   c->mega_ready = true;
   return TALOS_OK;
@@ -783,6 +794,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_mfma = env && env[0] == '1';
   env = getenv("TALOS_HIP_DOT4");
   c->allow_dot4 = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_DSPLIT");
+  c->allow_dsplit = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
