@@ -314,23 +314,27 @@ __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t
   return gw < total ? (int)((total - gw + tw - 1) / tw) : 0;
 }
 
-// One attention work item: KV head j, positions [t0, t1) of one slice
-// (src/model/llama.rs:139-155 for the GQA group of j).  The slice is walked
-// in sub-chunks of MEGA_ATTN_SUB positions with an online softmax (running
-// max m, running sum l, output rescaled by exp(m_old - m_new)); the K/V rows
-// of sub-chunk c+1 are loaded while sub-chunk c is computed (two register
-// buffers, loads unconditional with clamped rows so the wait counts stay
-// exact).  K uses 16 lanes per position (DPL dims each), V uses 4*DPL lanes
-// per position (a float4 each).  q, the K/V row at `pos` and the slice
-// partials are written once per launch (coherent stores) and read after the
-// barrier or the slice counter that follows the write.  With nsp > 1 slices
-// the last block to finish for head j merges them in slice order.
-// Short sequences (seq <= P.attn_direct) instead run one item per q head
-// over all positions (ng = 1, nsp = 1): no slice merge, and the group's K/V
-// rows, read by the group's items on one XCD, come from its L2.
-#define MEGA_ATTN_SUB 64
+// One attention work item: KV head j, q heads hq0..hq0+ng-1 (ng <=
+// MEGA_ATTN_HG), positions [t0, t1) of one slice (src/model/llama.rs:139-155
+// for those heads).  The slice is split into 8 contiguous ranges, one per
+// wave, and each wave runs its own online softmax with no block barrier:
+// steps of MEGA_ATTN_STEP positions, 16 lanes per position holding DPL
+// dimensions of its K row and of its V row, the next step's rows loaded
+// while this one computes (two register buffers; loads unconditional with
+// clamped rows, so the wait counts stay exact).  Scores are kept in log2
+// units (q.k * scale * log2 e), so every exponential is one exp2; row sums
+// use a mirror butterfly that leaves identical bits in all 16 lanes.  The
+// waves' (m, l, o) meet in LDS and are merged in wave order; with nsp > 1
+// slices the block publishes the slice partial and the last block to finish
+// for KV head j merges the slices in slice order.  q, the K/V row at `pos`
+// and the slice partials are written once per launch (coherent stores) and
+// read after the barrier or the slice counter that follows the write.
+// Short sequences (seq <= P.attn_direct) run one item per q head over all
+// positions (ng = 1, nsp = 1): no slice merge, and the group's K/V rows,
+// read by the group's items on one XCD, come from its L2.
+#define MEGA_ATTN_HG 4
+#define MEGA_ATTN_STEP 4
 
-static inline __host__ __device__ uint32_t mega_attn_ppr(uint32_t hd) { return MEGA_NT / (hd / 4); }
 // Positions per slice: ceil(seq * n_kv / nblocks) rounded up to 16 (at
 // least 16), so that the items (KV head x slice) cover about one per block.
 // As chunk >= seq * n_kv / nblocks, the slice count ceil(seq / chunk) is at
@@ -341,8 +345,21 @@ static inline __host__ __device__ int mega_attn_chunk(int seq, uint32_t n_kv, ui
   return c < 16 ? 16 : c;
 }
 static inline uint32_t mega_attn_max_splits(uint32_t n_kv, uint32_t nblocks) { return (nblocks + n_kv - 1) / n_kv; }
+// LDS floats: per wave and head its m and l, and its o row.
 static inline size_t mega_attn_lds_floats(uint32_t hd, uint32_t group) {
-  return (size_t)group * hd + (size_t)group * MEGA_ATTN_SUB + (size_t)mega_attn_ppr(hd) * group * hd + 64;
+  return (size_t)MEGA_NW * group * (hd + 2) + 64;
+}
+
+// Sum of the 16 lanes of a DPP row, the same bits in every lane (xor 1,
+// xor 2, half-mirror, mirror: each step adds two equal-bits halves).
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_HALF_MIRROR 0x141
+__device__ __forceinline__ float row_allsum16(float v) {
+  v += dpp_f<DPP_QUAD_1032>(0.f, v);
+  v += dpp_f<DPP_QUAD_2301>(0.f, v);
+  v += dpp_f<DPP_ROW_HALF_MIRROR>(0.f, v);
+  v += dpp_f<DPP_ROW_MIRROR>(0.f, v);
+  return v;
 }
 
 template <int DPL>
@@ -353,166 +370,181 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
   do {                                \
     if (tls >= 0) MEGA_MARK(P, tls + (k)); \
   } while (0)
-  constexpr int HD = 16 * DPL;            // head_dim
-  constexpr int TPP = HD / 4;             // V threads per position
-  constexpr int PPR = MEGA_NT / TPP;      // V positions per round
-  constexpr int VR = (MEGA_ATTN_SUB + PPR - 1) / PPR;
-  constexpr int KR = MEGA_ATTN_SUB / 32;  // K rounds of 32 positions
-  const uint32_t group = ng;  // the q heads hq0..hq0+ng-1 of this item (all of KV head j's when nsp > 1)
-  float* qs = smem;                                  // [group][HD]
-  float* sc = qs + group * HD;                       // [group][SUB]
-  float* ored = sc + group * MEGA_ATTN_SUB;          // [PPR][group][HD]
-  __shared__ float mh[TALOS_MAX_GROUP], lh[TALOS_MAX_GROUP], ah[TALOS_MAX_GROUP];
+  constexpr int HD = 16 * DPL;  // head_dim
+  constexpr int HG = MEGA_ATTN_HG;
+  constexpr int RS = MEGA_ATTN_STEP / 4;  // rounds of 4 positions per step
+  constexpr float kLog2e = 1.4426950408889634f;
+  const uint32_t group = ng;
+  float* mw = smem;                    // [NW][group]
+  float* lw = mw + MEGA_NW * group;    // [NW][group]
+  float* ow = lw + MEGA_NW * group;    // [NW][group][HD]
   __shared__ int am_last;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
+  const int dl = lane & 15, g = lane >> 4;
   const int seq = pos + 1;
   const int t0 = split * chunk;
   const int t1 = min(seq, t0 + chunk);  // t1 > t0: split < nsp = ceil(seq / chunk)
   const int len = t1 - t0;
-  const int nsub = (len + MEGA_ATTN_SUB - 1) / MEGA_ATTN_SUB;
-  const size_t hoff = (size_t)j * HD;
-  const int dl = lane & 15, slot = wave * 4 + (lane >> 4);  // K: lane group (16 lanes) per position
-  const int vp = tid / TPP, vd = tid % TPP;                 // V: TPP threads per position
-  const int vpc = vp < PPR ? vp : PPR - 1;
+  const int pw = (len + MEGA_NW - 1) / MEGA_NW;
+  const int w0 = t0 + wave * pw, w1 = min(t1, w0 + pw);  // this wave's positions (maybe none)
+  const int nsteps = w1 > w0 ? (w1 - w0 + MEGA_ATTN_STEP - 1) / MEGA_ATTN_STEP : 0;
+  const size_t hoff = (size_t)j * HD + (size_t)dl * DPL;
+  const float qscale = P.scale * kLog2e;
 
-  // Rows of sub-chunk c (clamped to the last sub-chunk and the last row of
-  // the slice: out-of-range lanes reload a row of this slice).
-  auto load = [&](float (&kr)[KR][DPL], f4 (&vr)[VR], int c) {
-    const int b = t0 + min(c, nsub - 1) * MEGA_ATTN_SUB;
+  float qr[HG][DPL];
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      const int t = min(b + r * 32 + slot, t1 - 1);
-      const float* kp = kc + (size_t)t * P.kv_dim + hoff + dl * DPL;
+  for (int h = 0; h < HG; ++h) {
+    const float* qp = qv + ((size_t)hq0 + (h < (int)ng ? h : 0)) * HD + dl * DPL;
+    if constexpr (DPL % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < DPL; i += 4) {
+        const f4 v = gld4(qp + i);
+        qr[h][i] = v.x * qscale;
+        qr[h][i + 1] = v.y * qscale;
+        qr[h][i + 2] = v.z * qscale;
+        qr[h][i + 3] = v.w * qscale;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) qr[h][i] = gld(qp + i) * qscale;
+    }
+  }
+  // rows of step s (clamped into the slice: out-of-range lanes reload a row
+  // of it and are masked)
+  auto load = [&](float (&kr)[RS][DPL], float (&vr)[RS][DPL], int s) {
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+      const int t = min(w0 + s * MEGA_ATTN_STEP + r * 4 + g, t1 - 1);
+      const float* kp = kc + (size_t)t * P.kv_dim + hoff;
+      const float* vp = vc + (size_t)t * P.kv_dim + hoff;
       if constexpr (DPL % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < DPL; i += 4) {
-          const f4 v = gld4(kp + i);
-          kr[r][i] = v.x;
-          kr[r][i + 1] = v.y;
-          kr[r][i + 2] = v.z;
-          kr[r][i + 3] = v.w;
+          const f4 a = gld4(kp + i), b = gld4(vp + i);
+          kr[r][i] = a.x;
+          kr[r][i + 1] = a.y;
+          kr[r][i + 2] = a.z;
+          kr[r][i + 3] = a.w;
+          vr[r][i] = b.x;
+          vr[r][i + 1] = b.y;
+          vr[r][i + 2] = b.z;
+          vr[r][i + 3] = b.w;
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) kr[r][i] = gld(kp + i);
+        for (int i = 0; i < DPL; ++i) {
+          kr[r][i] = gld(kp + i);
+          vr[r][i] = gld(vp + i);
+        }
       }
     }
-#pragma unroll
-    for (int r = 0; r < VR; ++r) {
-      const int t = min(b + r * PPR + vpc, t1 - 1);
-      vr[r] = gld4(vc + (size_t)t * P.kv_dim + hoff + vd * 4);
-    }
   };
-
-  f4 acc[TALOS_MAX_GROUP];
+  float m[HG], l[HG], acc[HG][DPL];
 #pragma unroll
-  for (int h = 0; h < TALOS_MAX_GROUP; ++h) acc[h] = f4{0.f, 0.f, 0.f, 0.f};
-
-  // Online softmax over sub-chunk c held in (kr, vr).
-  auto compute = [&](const float (&kr)[KR][DPL], const f4 (&vr)[VR], int c) {
-    const int slen = min(MEGA_ATTN_SUB, len - c * MEGA_ATTN_SUB);
-    // scores (a 16-lane group is one DPP row)
-#pragma unroll 1
-    for (int h = 0; h < (int)group; ++h) {
-      float qr[DPL];
+  for (int h = 0; h < HG; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) qr[i] = qs[h * HD + dl * DPL + i];
+    for (int i = 0; i < DPL; ++i) acc[h][i] = 0.f;
+  }
+  auto compute = [&](const float (&kr)[RS][DPL], const float (&vr)[RS][DPL], int s) {
+    float sc[HG][RS];
+    bool ok[RS];
 #pragma unroll
-      for (int r = 0; r < KR; ++r) {
-        const int tl = r * 32 + slot;
-        if (r * 32 >= slen) break;
+    for (int r = 0; r < RS; ++r) ok[r] = w0 + s * MEGA_ATTN_STEP + r * 4 + g < w1;
+#pragma unroll
+    for (int r = 0; r < RS; ++r)
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
         float d = 0.f;
+        if (h < (int)ng) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[i], kr[r][i], d);
-        d = row_sum16(d);
-        if (tl < slen && dl == 0) sc[h * MEGA_ATTN_SUB + tl] = d * P.scale;
-      }
-    }
-    __syncthreads();
-    // running statistics (one wave per head); sc becomes exp(s - m_new)
-    for (uint32_t h = wave; h < group; h += MEGA_NW) {
-      float mx = -INFINITY;
-      for (int t = lane; t < slen; t += 64) mx = fmaxf(mx, sc[h * MEGA_ATTN_SUB + t]);
-      mx = wave_max(mx);
-      const float m_old = c == 0 ? -INFINITY : mh[h];
-      const float m_new = fmaxf(m_old, mx);
-      float l = 0.f;
-      for (int t = lane; t < slen; t += 64) {
-        const float e = expf(sc[h * MEGA_ATTN_SUB + t] - m_new);
-        sc[h * MEGA_ATTN_SUB + t] = e;
-        l += e;
-      }
-      l = wave_sum(l);
-      if (lane == 0) {
-        const float a = c == 0 ? 0.f : expf(m_old - m_new);
-        ah[h] = a;
-        lh[h] = c == 0 ? l : __builtin_fmaf(lh[h], a, l);
-        mh[h] = m_new;
-      }
-    }
-    __syncthreads();
-    // o[h][4vd..4vd+3] over this thread's positions, rescaled
-    if (vp < PPR) {
-#pragma unroll
-      for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
-        if (h < (int)group) {
-          const float a = ah[h];
-          acc[h].x *= a;
-          acc[h].y *= a;
-          acc[h].z *= a;
-          acc[h].w *= a;
+          for (int i = 0; i < DPL; ++i) d = __builtin_fmaf(qr[h][i], kr[r][i], d);
+          d = row_allsum16(d);
         }
+        sc[h][r] = ok[r] ? d : -INFINITY;
       }
 #pragma unroll
-      for (int r = 0; r < VR; ++r) {
-        const int tl = r * PPR + vp;
-        if (tl < slen) {
+    for (int h = 0; h < HG; ++h) {
+      if (h >= (int)ng) continue;
+      float mx = sc[h][0];
 #pragma unroll
-          for (int h = 0; h < TALOS_MAX_GROUP; ++h) {
-            if (h < (int)group) {
-              const float p = sc[h * MEGA_ATTN_SUB + tl];
-              acc[h].x = __builtin_fmaf(p, vr[r].x, acc[h].x);
-              acc[h].y = __builtin_fmaf(p, vr[r].y, acc[h].y);
-              acc[h].z = __builtin_fmaf(p, vr[r].z, acc[h].z);
-              acc[h].w = __builtin_fmaf(p, vr[r].w, acc[h].w);
-            }
-          }
-        }
+      for (int r = 1; r < RS; ++r) mx = fmaxf(mx, sc[h][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, TALOS_WAVE));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, TALOS_WAVE));
+      const float mn = fmaxf(m[h], mx);
+      const float a = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[h] - mn);
+      m[h] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) acc[h][i] *= a;
+#pragma unroll
+      for (int r = 0; r < RS; ++r) {
+        const float p = ok[r] ? __builtin_amdgcn_exp2f(sc[h][r] - mn) : 0.f;
+        ps += p;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[h][i] = __builtin_fmaf(p, vr[r][i], acc[h][i]);
       }
+      l[h] = __builtin_fmaf(l[h], a, ps);
     }
-    __syncthreads();  // sc and ah are rewritten by the next sub-chunk
   };
 
-  float kA[KR][DPL], kB[KR][DPL];
-  f4 vA[VR], vB[VR];
+  float kA[RS][DPL], vA[RS][DPL], kB[RS][DPL], vB[RS][DPL];
   load(kA, vA, 0);
-  // q for the group's heads
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) qs[i] = gld(qv + (size_t)hq0 * HD + i);
-  __syncthreads();
   ATTN_MARK(0);
-  for (int c = 0; c < nsub; c += 2) {
-    load(kB, vB, c + 1);
-    compute(kA, vA, c);
-    if (c + 1 >= nsub) break;
-    load(kA, vA, c + 2);
-    compute(kB, vB, c + 1);
+  for (int s = 0; s < nsteps; s += 2) {
+    load(kB, vB, s + 1);
+    compute(kA, vA, s);
+    if (s + 1 >= nsteps) break;
+    load(kA, vA, s + 2);
+    compute(kB, vB, s + 1);
   }
   ATTN_MARK(1);
-  if (vp < PPR) {
+  // this wave's (m, l, o): l and o summed over the 4 row groups in a fixed
+  // order (the xor butterfly leaves the same bits in every lane)
 #pragma unroll
-    for (int h = 0; h < TALOS_MAX_GROUP; ++h)
-      if (h < (int)group) *reinterpret_cast<f4*>(ored + ((size_t)vp * group + h) * HD + vd * 4) = acc[h];
+  for (int h = 0; h < HG; ++h) {
+    if (h >= (int)ng) continue;
+    float lt = l[h];
+    lt += __shfl_xor(lt, 16, TALOS_WAVE);
+    lt += __shfl_xor(lt, 32, TALOS_WAVE);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      float o = acc[h][i];
+      o += __shfl_xor(o, 16, TALOS_WAVE);
+      o += __shfl_xor(o, 32, TALOS_WAVE);
+      acc[h][i] = o;
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) ow[((size_t)wave * group + h) * HD + dl * DPL + i] = acc[h][i];
+    }
+    if (lane == 0) {
+      mw[wave * group + h] = m[h];
+      lw[wave * group + h] = lt;
+    }
   }
   __syncthreads();
   ATTN_MARK(2);
-
-  if (nsp == 1) {
-    for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
-      const uint32_t h = i / HD, dd = i % HD;
-      float o = 0.f;
-      for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
-      st_coh(atty + ((size_t)hq0 + h) * HD + dd, o / lh[h]);
+  // merge the waves in wave order
+  float O = 0.f, M = -INFINITY, L = 0.f;
+  const int oi = tid;
+  const bool mine = oi < (int)(group * HD);
+  const int oh = mine ? oi / HD : 0, od = oi % HD;
+  if (mine) {
+#pragma unroll
+    for (int w = 0; w < MEGA_NW; ++w) M = fmaxf(M, mw[w * group + oh]);
+#pragma unroll
+    for (int w = 0; w < MEGA_NW; ++w) {
+      const float mv = mw[w * group + oh];
+      const float e = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - M);
+      L = __builtin_fmaf(lw[w * group + oh], e, L);
+      O = __builtin_fmaf(ow[((size_t)w * group + oh) * HD + od], e, O);
     }
+  }
+  if (nsp == 1) {
+    if (mine) st_coh(atty + ((size_t)hq0 + oh) * HD + od, O / L);
     __syncthreads();
     ATTN_MARK(4);
     return;
@@ -520,15 +552,12 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
 
   const size_t pstride = HD + 2;
   float* mypart = part + ((size_t)j * P.nsplit + split) * group * pstride;
-  for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
-    const uint32_t h = i / HD, dd = i % HD;
-    float o = 0.f;
-    for (int s = 0; s < PPR; ++s) o += ored[((size_t)s * group + h) * HD + dd];
-    st_coh(mypart + h * pstride + dd, o);
-  }
-  if (tid < (int)group) {
-    st_coh(mypart + tid * pstride + HD, mh[tid]);
-    st_coh(mypart + tid * pstride + HD + 1, lh[tid]);
+  if (mine) {
+    st_coh(mypart + oh * pstride + od, O);
+    if (od == 0) {
+      st_coh(mypart + oh * pstride + HD, M);
+      st_coh(mypart + oh * pstride + HD + 1, L);
+    }
   }
   wait_mem();
   __syncthreads();
@@ -546,7 +575,7 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
     constexpr int MB = 16;
     for (uint32_t i = tid; i < group * HD; i += MEGA_NT) {
       const uint32_t h = i / HD, dd = i % HD;
-      float M = -INFINITY, L = 0.f, O = 0.f;
+      float Ms = -INFINITY, Ls = 0.f, Os = 0.f;
       for (int s0 = 0; s0 < nsp; s0 += MB) {
         float ov[MB], mv[MB], lv[MB];
 #pragma unroll
@@ -556,23 +585,23 @@ __device__ __forceinline__ void mega_attn_item(const MegaParams& P, const float*
           mv[r] = gld(ps + HD);
           lv[r] = gld(ps + HD + 1);
         }
-        float Mb = M;
+        float Mb = Ms;
 #pragma unroll
         for (int r = 0; r < MB; ++r)
           if (s0 + r < nsp) Mb = fmaxf(Mb, mv[r]);
-        const float a = expf(M - Mb);  // 0 for the first batch (M = -inf)
-        L *= a;
-        O *= a;
+        const float a = Ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Ms - Mb);  // 0 for the first batch
+        Ls *= a;
+        Os *= a;
 #pragma unroll
         for (int r = 0; r < MB; ++r)
           if (s0 + r < nsp) {
-            const float w = expf(mv[r] - Mb);
-            L = __builtin_fmaf(lv[r], w, L);
-            O = __builtin_fmaf(ov[r], w, O);
+            const float w = __builtin_amdgcn_exp2f(mv[r] - Mb);
+            Ls = __builtin_fmaf(lv[r], w, Ls);
+            Os = __builtin_fmaf(ov[r], w, Os);
           }
-        M = Mb;
+        Ms = Mb;
       }
-      st_coh(atty + ((size_t)hq0 + h) * HD + dd, O / L);
+      st_coh(atty + ((size_t)hq0 + h) * HD + dd, Os / Ls);
     }
     if (tid == 0) st_coh_u(P.count + j, 0u);
   }
@@ -589,7 +618,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   constexpr bool MF = MM == MEGA_MM_MFMA;
   constexpr bool IQ = MM == MEGA_MM_DOT4;
   constexpr bool IQO = IQ && (OF == TALOS_FMT_Q4_0 || OF == TALOS_FMT_Q8_0);  // the head too
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform: scalar registers
   const uint32_t nb = gridDim.x;
   const uint32_t gw = blockIdx.x * MEGA_NW + wave, tw = nb * MEGA_NW;
   GridSync G;

@@ -631,8 +631,10 @@ int mega_setup(talos_hip_ctx* c) {
   hipDeviceProp_t prop;
   HIPCHK(c, hipGetDeviceProperties(&prop, dev));
   // Shapes the persistent kernel handles: batched staging of up to
-  // MEGA_STAGE_MAX floats, head_dim a multiple of 16.
-  if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX || c->hd % 16) {
+  // MEGA_STAGE_MAX floats, head_dim a multiple of 16, at most MEGA_ATTN_HG
+  // q heads per KV head.
+  if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX || c->hd % 16 ||
+      c->group > MEGA_ATTN_HG) {
     c->mega_ready = true;
     return TALOS_OK;
   }
@@ -697,7 +699,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.tokens = c->tokens;
   P.sync = c->d_sync;
   P.nsplit = msplit;
-  P.max_chunk = MEGA_ATTN_SUB;
+  P.max_chunk = MEGA_ATTN_STEP;
   P.attn_direct = c->attn_direct;
   {
     // split down-projection: whole quarters of the row chunks that fit one
