@@ -198,7 +198,7 @@ def main() -> int:
     for p, tok in enumerate(prompt):
         model.forward_token(tok, p, want_logits=False)
     t1 = time.perf_counter()
-    npc = 32
+    npc = min(32, args.steps)
     for i in range(npc):
         lg = model.forward_gpu(int(toks[i]), P + i)
     pcie_tok_s = npc / (time.perf_counter() - t1)
