@@ -68,6 +68,7 @@ def lib() -> C.CDLL:
             "tor_model_reset": (None, [C.c_void_p]),
             "tor_model_kv_len": (C.c_size_t, [C.c_void_p]),
             "tor_model_set_kv": (C.c_int, [C.c_void_p, _F, _F, C.c_size_t]),
+            "tor_model_get_kv": (C.c_int, [C.c_void_p, _F, _F, C.c_size_t]),
             "tor_gguf_parse": (C.c_void_p, [C.c_void_p, C.c_size_t, C.c_char_p, C.c_size_t]),
             "tor_gguf_free": (None, [C.c_void_p]),
             "tor_gguf_get_u32": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint32)]),
@@ -241,6 +242,16 @@ class OracleModel:
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         lib().tor_model_set_kv(self._h, _f(k), _f(v), k.shape[1])
+
+    def get_kv(self, n_pos: int):
+        """K and V of the first n_pos cached positions, [layer, pos, kv_dim]."""
+        c = self.cfg
+        kvd = c.n_head_kv * (c.n_embd // c.n_head)
+        k = np.empty((c.n_layer, n_pos, kvd), np.float32)
+        v = np.empty_like(k)
+        if lib().tor_model_get_kv(self._h, _f(k), _f(v), n_pos) != 0:
+            raise ValueError(f"only {self.kv_len()} positions cached")
+        return k, v
 
 
 class OracleGguf:

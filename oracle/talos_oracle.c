@@ -840,6 +840,16 @@ int tor_model_set_kv(tor_model *m, const float *k, const float *v, size_t len) {
   return 0;
 }
 
+int tor_model_get_kv(const tor_model *m, float *k, float *v, size_t len) {
+  size_t kvd = (size_t)m->cfg.n_head_kv * (m->cfg.n_embd / m->cfg.n_head);
+  if (len > m->kv_len) return -1;
+  for (uint32_t l = 0; l < m->cfg.n_layer; ++l) {
+    memcpy(k + (size_t)l * len * kvd, m->kc[l], len * kvd * 4);
+    memcpy(v + (size_t)l * len * kvd, m->vc[l], len * kvd * 4);
+  }
+  return 0;
+}
+
 static void qmatvec(const tor_model *m, const qtensor *t, const float *x, float *out) {
   tor_matvec_quant(t->bytes, t->type, x, out, t->rows, t->cols, m->nthreads);
 }

@@ -119,6 +119,8 @@ size_t tor_model_kv_len(const tor_model *m);
  * prefix the GPU filled. */
 int tor_model_set_kv(tor_model *m, const float *k, const float *v,
                      size_t len);
+/* Copy the first `len` cached positions out, in the same layout. */
+int tor_model_get_kv(const tor_model *m, float *k, float *v, size_t len);
 
 #ifdef __cplusplus
 }

@@ -236,3 +236,31 @@ def test_reset_and_cap_context():
     m.cap_context(8)
     assert m.cfg.context_length == 8
     m.close()
+
+
+def test_kv_injection_resumes_the_forward():
+    """set_kv / get_kv use the forward's own cache layout [layer][pos][kv_dim]:
+    a second model started from the first one's cache continues bit for bit,
+    and position 0's K row of layer 0 is Wk . rmsnorm(embedding) (RoPE at
+    position 0 is the identity)."""
+    rng = np.random.default_rng(21)
+    W = rand_model(rng, **SHAPE, scale=0.3)
+    data = gguf_of(W, **SHAPE)
+    a, b = O.OracleModel(data), O.OracleModel(data)
+    toks = [3, 1, 4, 1, 5]
+    for p, t in enumerate(toks):
+        a.forward(t, p)
+    k, v = a.get_kv(len(toks))
+    assert k.shape == (SHAPE["n_layer"], len(toks), SHAPE["n_head_kv"] * SHAPE["embd"] // SHAPE["n_head"])
+    x = W["token_embd.weight"][toks[0]].astype(np.float64)
+    xn = x / np.sqrt(np.mean(x * x) + 1e-5) * W["blk.0.attn_norm.weight"]
+    np.testing.assert_allclose(k[0, 0], W["blk.0.attn_k.weight"].astype(np.float64) @ xn, atol=1e-5)
+    np.testing.assert_allclose(v[0, 0], W["blk.0.attn_v.weight"].astype(np.float64) @ xn, atol=1e-5)
+    b.set_kv(k, v)
+    assert b.kv_len() == len(toks)
+    la, lb = a.forward(9, len(toks)), b.forward(9, len(toks))
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    with pytest.raises(ValueError):
+        a.get_kv(99)
+    a.close()
+    b.close()
