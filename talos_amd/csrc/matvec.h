@@ -18,6 +18,14 @@
 #include "device_common.h"
 #include "layout.h"
 
+// Per 32-element block of x staged as int8 planes: the plane scale s
+// (x ~= s * (a + b/254 + c/254^2)) and the integer sums of the a, b and c
+// planes over the block.
+struct XBlk {
+  float s;
+  int sa, sb, sc;
+};
+
 // LDS index of x element e in layout L (0: pad 4 floats per 32; 1: per 64).
 template <int L>
 __device__ __forceinline__ int xidx(int e) {

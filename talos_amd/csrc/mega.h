@@ -218,6 +218,14 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
 // MEGA_DSPLIT waves may own.
 #define MEGA_DSPLIT 4
 #define MEGA_DSPLIT_ROWS 16
+// Items in flight in the gate/up and split down-projection streams (Q4_0
+// weights; the Q8_0 buffers are twice as large and keep two).
+#ifndef MEGA_DEPTH_GU
+#define MEGA_DEPTH_GU 3
+#endif
+#ifndef MEGA_DEPTH_D
+#define MEGA_DEPTH_D 2
+#endif
 
 // stage_xq with the fewest rounds of 8 elements per thread covering n.
 template <class Src, class After, class Wait>
@@ -911,8 +919,9 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      mv_stream<LF, RG, UN, true, IQ>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
-                                  pre);
+      constexpr int DG = IQ && LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_GU : 2;
+      mv_stream<LF, RG, UN, true, IQ, DG>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
+                                          pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
     // ---- down-projection (2-row units keep the long rows' double buffer in
@@ -1009,7 +1018,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           };
           XI xq = X.src(LL);
           xq.c0 = part * (int)qn;
-          mv_stream<LF, RD, UN, false, true>((int)(rpt / RD), unit, arrive, stage, epi, xq, lane, pre);
+          constexpr int DD = LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_D : 2;
+          mv_stream<LF, RD, UN, false, true, DD>((int)(rpt / RD), unit, arrive, stage, epi, xq, lane, pre);
           __syncthreads();
           if (threadIdx.x < TEAMS * rpt) {
             const uint32_t t = threadIdx.x / rpt, r = threadIdx.x % rpt;

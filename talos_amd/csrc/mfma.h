@@ -7,7 +7,8 @@
 // exact:
 //  * x (f32) is staged per 32-element block b as three int8 planes with a
 //    scale: x ~= s_b * (a + b'/254 + c/254^2), a, b', c in [-127, 127]
-//    (error <= 2^-24 * max|x_b|: f32-level), plus sum_b = sum of x over b;
+//    (error <= 2^-24 * max|x_b|: f32-level), plus each plane's integer sum
+//    over b;
 //  * a wave owns 16 weight rows (the MFMA's 16 columns).  In one MFMA lane
 //    group g (lanes 16g..16g+15) supplies 16 quants of its own Q4_0 block
 //    (the low or the high nibbles, as unsigned bytes 0..15), and the A
@@ -15,8 +16,8 @@
 //    other groups' k ranges), so D rows 4g..4g+2 are the block's three exact
 //    integer piece dots, in the registers of the lanes that own the block;
 //  * each lane then applies the block's scales in f32:
-//    acc += d * (s * (D0 + D1/254 + D2/254^2) - 8 * sum_b)
-//    (the -8 offset of Q4_0, src/gguf/dtype.rs:83-90, folded through sum_b).
+//    acc += d * s * (D0' + D1'/254 + D2'/254^2), Dp' = Dp - 8 * (plane sum)
+//    (the -8 offset of Q4_0, src/gguf/dtype.rs:83-90, exact in integers).
 // The K dimension of a row group is split over the block's 8 waves; partial
 // row sums meet in LDS and are added in wave order (deterministic).
 #pragma once
@@ -28,7 +29,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // LDS of the int8-plane staging (carve_xq).
 struct XQ {
   int8_t* pl;     // [3][nb][32]
-  float2* bs;     // [nb]: (s, sum of x) per block
+  XBlk* bs;       // [nb]
   int8_t* zero;   // 16 zero bytes (A rows that carry no plane)
   float* part;    // [MEGA_NW][gpb][16] per-wave partial row sums
   float* red;     // block-reduction scratch
@@ -37,7 +38,7 @@ struct XQ {
 
 static inline __host__ __device__ size_t xq_lds_bytes(int n, int gpb_max, int nwaves) {
   const size_t nb = (size_t)n / 32;
-  return nb * 96 + nb * 8 + 16 + (size_t)nwaves * gpb_max * 16 * 4 + 64 + 64;
+  return nb * 96 + nb * sizeof(XBlk) + 16 + (size_t)nwaves * gpb_max * 16 * 4 + 64 + 64;
 }
 
 __device__ __forceinline__ XQ carve_xq(float* smem, int n, int gpb_max, int nwaves) {
@@ -46,8 +47,8 @@ __device__ __forceinline__ XQ carve_xq(float* smem, int n, int gpb_max, int nwav
   uint8_t* p = reinterpret_cast<uint8_t*>(smem);
   X.pl = reinterpret_cast<int8_t*>(p);
   p += (size_t)X.nb * 96;
-  X.bs = reinterpret_cast<float2*>(p);
-  p += (size_t)X.nb * 8;
+  X.bs = reinterpret_cast<XBlk*>(p);
+  p += (size_t)X.nb * sizeof(XBlk);
   X.zero = reinterpret_cast<int8_t*>(p);
   p += 16;
   X.part = reinterpret_cast<float*>(p);
@@ -141,18 +142,15 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
 #pragma unroll
       for (int k = 0; k < 8; ++k) x[k] = x[k] * scale * wx[k];
     }
-    float am = 0.f, sm = 0.f;
+    float am = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      am = fmaxf(am, fabsf(x[k]));
-      sm += x[k];
-    }
+    for (int k = 0; k < 8; ++k) am = fmaxf(am, fabsf(x[k]));
     // the block is the quad of threads 4m..4m+3
     am = fmaxf(am, dpp_f<DPP_QUAD_1032>(am, am));
     am = fmaxf(am, dpp_f<DPP_QUAD_2301>(am, am));
-    sm = quad_sum(sm);
     const float inv = am > 0.f ? 127.f / am : 0.f;
     uint32_t pa[2], pb[2], pc[2];
+    float sa = 0.f, sb = 0.f, sc = 0.f;  // plane sums: integers below 2^12, exact
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       // t - a is exact, so fma(t, 254, -254 a) is (t - a) * 254 rounded
@@ -166,6 +164,9 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
         const float t2 = __builtin_fmaf(t, 254.f, -254.f * a);
         const float b = rne(t2);
         const float c = rne(__builtin_fmaf(t2, 254.f, -254.f * b));
+        sa += a;
+        sb += b;
+        sc += c;
         wa = __builtin_amdgcn_cvt_pk_u8_f32(a + 128.f, k, wa);
         wb = __builtin_amdgcn_cvt_pk_u8_f32(b + 128.f, k, wb);
         wc = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.f, k, wc);
@@ -174,6 +175,9 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
       pb[hh] = wb ^ 0x80808080u;
       pc[hh] = wc ^ 0x80808080u;
     }
+    sa = quad_sum(sa);
+    sb = quad_sum(sb);
+    sc = quad_sum(sc);
     if (ok) {
       const int blk = g8 >> 2, off = (g8 & 3) * 8;
       const size_t plane = (size_t)X.nb * 32;
@@ -181,7 +185,7 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
       *reinterpret_cast<uint2*>(X.pl + at) = uint2{pa[0], pa[1]};
       *reinterpret_cast<uint2*>(X.pl + plane + at) = uint2{pb[0], pb[1]};
       *reinterpret_cast<uint2*>(X.pl + 2 * plane + at) = uint2{pc[0], pc[1]};
-      if ((g8 & 3) == 0) X.bs[blk] = float2{am / 127.f, sm};
+      if ((g8 & 3) == 0) X.bs[blk] = XBlk{am / 127.f, (int)sa, (int)sb, (int)sc};
     }
   }
   __syncthreads();
@@ -240,10 +244,11 @@ __device__ __forceinline__ float mq_compute(const MqBuf<U>& B, const XQ& X, int 
     const v4i a1 = *reinterpret_cast<const v4i*>(ahi);
     v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, nib_lo(B.q[u]), zero4, 0, 0, 0);
     D = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, nib_hi(B.q[u]), D, 0, 0, 0);
-    const float2 sx = X.bs[blk];
-    const float f = __builtin_fmaf((float)D[2], k2, __builtin_fmaf((float)D[1], k1, (float)D[0]));
+    const XBlk sx = X.bs[blk];
+    const float f = __builtin_fmaf((float)(D[2] - 8 * sx.sc), k2,
+                                   __builtin_fmaf((float)(D[1] - 8 * sx.sb), k1, (float)(D[0] - 8 * sx.sa)));
     const float d = f16_to_f32((uint16_t)B.sc[u]);
-    acc = __builtin_fmaf(d, __builtin_fmaf(sx.x, f, -8.f * sx.y), acc);
+    acc = __builtin_fmaf(d, sx.s * f, acc);
   }
   return acc;
 }

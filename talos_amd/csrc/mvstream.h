@@ -79,7 +79,7 @@ __device__ __forceinline__ void mv_load(MvBuf<FMT, R, U>& B, const DevMat& A0, c
 
 // The staged x a matvec reads: f32 values (XF: xs in the xidx layout of
 // the format, xsum per 16 elements), or int8 planes (XI, Q4_0/Q8_0 only:
-// the [3][2][nb] 16-byte words and (s, sum) per 32-element block of
+// the [3][2][nb] 16-byte words and the XBlk per 32-element block of
 // stage_xq with SPLIT).
 struct XF {
   const float* xs;
@@ -87,7 +87,7 @@ struct XF {
 };
 struct XI {
   const uint8_t* pl;
-  const float2* bs;
+  const XBlk* bs;
   int nb;
   int c0;  // chunk c of the matvec reads block c0 + c of x
 };
@@ -152,23 +152,28 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XF& 
 
 // acc[i] += <row slot i, x> with x as three int8 planes:
 // x_e = s_b * (a_e + b_e/254 + c_e/254^2) for the elements e of block b
-// (error <= 2^-24 * max|x_b|, f32-level).  The integer piece dots are exact
-// (v_dot4_i32_i8: Q4_0 nibbles 0..15 or Q8_0 quants times plane bytes);
-// the block then contributes d * (s/254 * ((254 A + B) + C/254) - off * sum_b)
-// with off = 8 for Q4_0 (its -8, src/gguf/dtype.rs:83-90) and 0 for Q8_0.
+// (error <= 2^-24 * max|x_b|, f32-level).  The piece dots with the signed
+// quants w (Q4_0: nibble - 8, src/gguf/dtype.rs:83-90; Q8_0: the byte) are
+// exact integers: v_dot4_i32_i8 of the raw nibbles 0..15 (or Q8_0 bytes)
+// against a plane, its chain started at -8 * (plane sum over the block) for
+// Q4_0, so A = sum(w a), B = sum(w b), C = sum(w c) come out offset-free.
+// 254 A + B is formed in the B chain's start (|A| < 2^16, v_mad_i32_i24),
+// so a block costs three dot4 chains and one float combine:
+//   acc += d * (s/254) * ((254 A + B) + C/254).
 __device__ __forceinline__ int dot4_i8(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// One lane's x for one chunk-step: the chunk's three planes and its
-// (s/254, -off * sum_b).
+// One lane's x for one chunk-step: the chunk's three planes, s/254 (0 for a
+// chunk past the row end, which then adds nothing) and the chain starts.
 struct XIr {
   u4 pw[3][2];
-  float s254, off;
+  float s254;
+  int ia, ib, ic;
 };
 
 template <uint32_t FMT>
-__device__ __forceinline__ XIr xi_fetch(const XI& X, int cc) {
+__device__ __forceinline__ XIr xi_fetch(const XI& X, int cc, bool ok) {
   XIr r;
   cc += X.c0;
   const size_t plane = (size_t)X.nb * 32;
@@ -177,86 +182,80 @@ __device__ __forceinline__ XIr xi_fetch(const XI& X, int cc) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
       r.pw[p][h] = *reinterpret_cast<const u4*>(X.pl + p * plane + ((size_t)h * X.nb + cc) * 16);
-  const float2 sx = X.bs[cc];
-  r.s254 = sx.x * (1.0f / 254.0f);
-  r.off = FMT == TALOS_FMT_Q4_0 ? -8.f * sx.y : 0.f;
+  const XBlk sx = X.bs[cc];
+  r.s254 = ok ? sx.s * (1.0f / 254.0f) : 0.f;
+  constexpr int off = FMT == TALOS_FMT_Q4_0 ? -8 : 0;
+  r.ia = off * sx.sa;
+  r.ib = off * sx.sb;
+  r.ic = off * sx.sc;
   return r;
 }
 
-// acc[i] += row slot i of chunk-step u against x.  Rows go in pairs; each
-// plane's 8 dot4 run as two chains (4 + 4, summed exactly as integers), so
-// 12 independent chains keep the VALU busy.
+// acc[i] += row slot i of chunk-step u against x.  Per row two chains (the
+// a-then-b chain and the c chain), interleaved over the R rows.
 template <uint32_t FMT, int R, int U>
-__device__ __forceinline__ void xi_dot(const MvBuf<FMT, R, U>& B, int u, const XIr& x, bool ok, float (&acc)[R]) {
+__device__ __forceinline__ void xi_dot(const MvBuf<FMT, R, U>& B, int u, const XIr& x, float (&acc)[R]) {
   static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "int8-plane x is for Q4_0 / Q8_0");
   constexpr float k254 = 1.0f / 254.0f;
-  constexpr int RP = R >= 2 ? 2 : 1;
+  uint32_t w[R][8];
 #pragma unroll
-  for (int i0 = 0; i0 < R; i0 += RP) {
-    uint32_t w[RP][8];
-#pragma unroll
-    for (int j = 0; j < RP; ++j) {
-      const int i = i0 + j;
-      if (FMT == TALOS_FMT_Q4_0) {
-        const u4 q = B.q[i][u][0];
-        w[j][0] = q.x & 0x0F0F0F0Fu;
-        w[j][1] = q.y & 0x0F0F0F0Fu;
-        w[j][2] = q.z & 0x0F0F0F0Fu;
-        w[j][3] = q.w & 0x0F0F0F0Fu;
-        w[j][4] = (q.x >> 4) & 0x0F0F0F0Fu;
-        w[j][5] = (q.y >> 4) & 0x0F0F0F0Fu;
-        w[j][6] = (q.z >> 4) & 0x0F0F0F0Fu;
-        w[j][7] = (q.w >> 4) & 0x0F0F0F0Fu;
-      } else {  // the device layout keeps Q8_0 quants biased by 128 (q ^ 0x80)
-        const u4 q0 = B.q[i][u][0], q1 = B.q[i][u][MvT<FMT>::QW - 1];
-        w[j][0] = q0.x ^ 0x80808080u;
-        w[j][1] = q0.y ^ 0x80808080u;
-        w[j][2] = q0.z ^ 0x80808080u;
-        w[j][3] = q0.w ^ 0x80808080u;
-        w[j][4] = q1.x ^ 0x80808080u;
-        w[j][5] = q1.y ^ 0x80808080u;
-        w[j][6] = q1.z ^ 0x80808080u;
-        w[j][7] = q1.w ^ 0x80808080u;
-      }
+  for (int i = 0; i < R; ++i) {
+    if (FMT == TALOS_FMT_Q4_0) {
+      const u4 q = B.q[i][u][0];
+      w[i][0] = q.x & 0x0F0F0F0Fu;
+      w[i][1] = q.y & 0x0F0F0F0Fu;
+      w[i][2] = q.z & 0x0F0F0F0Fu;
+      w[i][3] = q.w & 0x0F0F0F0Fu;
+      w[i][4] = (q.x >> 4) & 0x0F0F0F0Fu;
+      w[i][5] = (q.y >> 4) & 0x0F0F0F0Fu;
+      w[i][6] = (q.z >> 4) & 0x0F0F0F0Fu;
+      w[i][7] = (q.w >> 4) & 0x0F0F0F0Fu;
+    } else {  // the device layout keeps Q8_0 quants biased by 128 (q ^ 0x80)
+      const u4 q0 = B.q[i][u][0], q1 = B.q[i][u][MvT<FMT>::QW - 1];
+      w[i][0] = q0.x ^ 0x80808080u;
+      w[i][1] = q0.y ^ 0x80808080u;
+      w[i][2] = q0.z ^ 0x80808080u;
+      w[i][3] = q0.w ^ 0x80808080u;
+      w[i][4] = q1.x ^ 0x80808080u;
+      w[i][5] = q1.y ^ 0x80808080u;
+      w[i][6] = q1.z ^ 0x80808080u;
+      w[i][7] = q1.w ^ 0x80808080u;
     }
-    int lo[RP][3], hi[RP][3];
+  }
+  // plane word k of the lane's chunk: element order of the quants above
+  auto xw = [&](int p, int k) {
+    const u4& v = x.pw[p][k >> 2];
+    return (k & 3) == 0 ? v.x : (k & 3) == 1 ? v.y : (k & 3) == 2 ? v.z : v.w;
+  };
+  int ab[R], c[R];
 #pragma unroll
-    for (int j = 0; j < RP; ++j)
+  for (int i = 0; i < R; ++i) {
+    ab[i] = x.ia;
+    c[i] = x.ic;
+  }
+  // the c chain runs half beside the a chain, half beside the b chain
 #pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        lo[j][p] = dot4_i8(w[j][0], x.pw[p][0].x, 0);
-        hi[j][p] = dot4_i8(w[j][4], x.pw[p][1].x, 0);
-      }
+  for (int k = 0; k < 8; ++k)
 #pragma unroll
-    for (int j = 0; j < RP; ++j)
-#pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        lo[j][p] = dot4_i8(w[j][1], x.pw[p][0].y, lo[j][p]);
-        hi[j][p] = dot4_i8(w[j][5], x.pw[p][1].y, hi[j][p]);
-      }
-#pragma unroll
-    for (int j = 0; j < RP; ++j)
-#pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        lo[j][p] = dot4_i8(w[j][2], x.pw[p][0].z, lo[j][p]);
-        hi[j][p] = dot4_i8(w[j][6], x.pw[p][1].z, hi[j][p]);
-      }
-#pragma unroll
-    for (int j = 0; j < RP; ++j)
-#pragma unroll
-      for (int p = 0; p < 3; ++p) {
-        lo[j][p] = dot4_i8(w[j][3], x.pw[p][0].w, lo[j][p]);
-        hi[j][p] = dot4_i8(w[j][7], x.pw[p][1].w, hi[j][p]);
-      }
-#pragma unroll
-    for (int j = 0; j < RP; ++j) {
-      const int i = i0 + j;
-      const int a = lo[j][0] + hi[j][0], b = lo[j][1] + hi[j][1], c = lo[j][2] + hi[j][2];
-      // |a| <= 32 * 128 * 127, so 254 * a + b fits an int32
-      const float t = __builtin_fmaf((float)c, k254, (float)(a * 254 + b));
-      const float d = ok ? f16_to_f32((uint16_t)B.a[i][u]) : 0.f;
-      acc[i] = __builtin_fmaf(d, __builtin_fmaf(x.s254, t, x.off), acc[i]);
+    for (int i = 0; i < R; ++i) {
+      ab[i] = dot4_i8(w[i][k], xw(0, k), ab[i]);
+      if (k < 4) c[i] = dot4_i8(w[i][k], xw(2, k), c[i]);
     }
+  // |A| <= 32 * 128 * 127 < 2^23: a 24-bit multiply-add starts the b chain
+#pragma unroll
+  for (int i = 0; i < R; ++i) ab[i] = __mul24(ab[i], 254) + x.ib;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      ab[i] = dot4_i8(w[i][k], xw(1, k), ab[i]);
+      if (k >= 4) c[i] = dot4_i8(w[i][k], xw(2, k), c[i]);
+    }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const float t = __builtin_fmaf((float)c[i], k254, (float)ab[i]);
+    const float d = f16_to_f32((uint16_t)B.a[i][u]);
+    acc[i] = __builtin_fmaf(d, x.s254 * t, acc[i]);
   }
 }
 
@@ -268,12 +267,13 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XI& 
     const int c = c0 + u * TALOS_WAVE + lane;
     return c < nc ? c : nc - 1;
   };
-  XIr x = xi_fetch<FMT>(X, cc(0));
+  auto ok = [&](int u) { return c0 + u * TALOS_WAVE + lane < nc; };
+  XIr x = xi_fetch<FMT>(X, cc(0), ok(0));
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     XIr xn;
-    if (u + 1 < U) xn = xi_fetch<FMT>(X, cc(u + 1));
-    xi_dot<FMT, R, U>(B, u, x, c0 + u * TALOS_WAVE + lane < nc, acc);
+    if (u + 1 < U) xn = xi_fetch<FMT>(X, cc(u + 1), ok(u + 1));
+    xi_dot<FMT, R, U>(B, u, x, acc);
     if (u + 1 < U) x = xn;
   }
 }
@@ -283,14 +283,13 @@ __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XI& 
 template <int U>
 struct XIreg {
   XIr x[U];
-  bool ok[U];
 };
 
 template <uint32_t FMT, int R, int U>
 __device__ __forceinline__ void mv_compute(const MvBuf<FMT, R, U>& B, const XIreg<U>& X, int, int, int,
                                            float (&acc)[R]) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) xi_dot<FMT, R, U>(B, u, X.x[u], X.ok[u], acc);
+  for (int u = 0; u < U; ++u) xi_dot<FMT, R, U>(B, u, X.x[u], acc);
 }
 
 // Run this wave's units.  unit(k, &A0, &A1, &r0, &rmax) describes the k-th
@@ -303,13 +302,21 @@ __device__ __forceinline__ void mv_run(int nitems, int iters, int nc, UnitFn& un
                                        MvBuf<FMT, R, U>& b0, MvBuf<FMT, R, U>& b1, const DevMat& A0, const DevMat& A1,
                                        uint32_t r0, uint32_t rmax);
 
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class EpiFn, class XS>
+__device__ __forceinline__ void mv_run3(int nitems, int iters, int nc, UnitFn& unit, EpiFn& epi, const XS& xs,
+                                        int lane, MvBuf<FMT, R, U>& b0, MvBuf<FMT, R, U>& b1, DevMat N0, DevMat N1,
+                                        uint32_t nr0, uint32_t nrmax);
+
 // XREG (int8-plane x only): the caller guarantees a row fits one item
 // (nchunk <= U * 64), so a lane's x is the same for every item and is read
 // from LDS once, into registers.
-template <uint32_t FMT, int R, int U, bool PAIR, bool XREG = false, class UnitFn, class ArriveFn, class StageFn,
-          class EpiFn, class XS>
+// DEPTH: items in flight, 2 (compute item i while item i+1 loads) or 3
+// (items i+1 and i+2 load; the first two are issued at pf).
+template <uint32_t FMT, int R, int U, bool PAIR, bool XREG = false, int DEPTH = 2, class UnitFn, class ArriveFn,
+          class StageFn, class EpiFn, class XS>
 __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
                                           const XS& xs, int lane, bool pre) {
+  static_assert(DEPTH == 2 || DEPTH == 3, "two or three items in flight");
   // Every weight load below is issued unconditionally (an idle wave's first
   // load reads row 0, discarded): the compiler's wait counts then stay exact,
   // so computing item i waits only for item i's loads, never for item i+1's
@@ -326,25 +333,100 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arri
     rmax = 1;
   }
   arrive();
-  auto pf = [&] { mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane); };
+  const int nitems = nunits > 0 ? nunits * iters : 0;
+  // DEPTH 3: item 1 (item 0 again when there is no second item) goes into
+  // b1 with item 0, so both loads are unconditional.
+  DevMat N0 = A0, N1 = A1;
+  uint32_t nr0 = r0, nrmax = rmax;
+  auto pf = [&] {
+    mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
+    if constexpr (DEPTH == 3) {
+      const bool two = nitems > 1;
+      if (two && iters == 1) unit(1, N0, N1, nr0, nrmax);
+      mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, two && iters > 1 ? U * TALOS_WAVE : 0, lane);
+    }
+  };
   if (pre) {
     stage(pf);
   } else {
     stage([] {});
     pf();
   }
-  const int nitems = nunits > 0 ? nunits * iters : 0;
   if constexpr (XREG) {
     XIreg<U> xr;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = u * TALOS_WAVE + lane;
-      xr.ok[u] = c < nc;
-      xr.x[u] = xi_fetch<FMT>(xs, c < nc ? c : nc - 1);
+      xr.x[u] = xi_fetch<FMT>(xs, c < nc ? c : nc - 1, c < nc);
     }
-    mv_run<FMT, R, U, PAIR>(nitems, 1, nc, unit, epi, xr, lane, b0, b1, A0, A1, r0, rmax);
+    if constexpr (DEPTH == 3)
+      mv_run3<FMT, R, U, PAIR>(nitems, 1, nc, unit, epi, xr, lane, b0, b1, N0, N1, nr0, nrmax);
+    else
+      mv_run<FMT, R, U, PAIR>(nitems, 1, nc, unit, epi, xr, lane, b0, b1, A0, A1, r0, rmax);
   } else {
-    mv_run<FMT, R, U, PAIR>(nitems, iters, nc, unit, epi, xs, lane, b0, b1, A0, A1, r0, rmax);
+    if constexpr (DEPTH == 3)
+      mv_run3<FMT, R, U, PAIR>(nitems, iters, nc, unit, epi, xs, lane, b0, b1, N0, N1, nr0, nrmax);
+    else
+      mv_run<FMT, R, U, PAIR>(nitems, iters, nc, unit, epi, xs, lane, b0, b1, A0, A1, r0, rmax);
+  }
+}
+
+// The item loop with three items in flight: items 0 and 1 are already
+// issued into b0 and b1 (N0/N1/nr0/nrmax describe item 1's unit); item i+2
+// is issued before item i is computed.  Each tail is straight-line code, so
+// every wait count stays exact.
+template <uint32_t FMT, int R, int U, bool PAIR, class UnitFn, class EpiFn, class XS>
+__device__ __forceinline__ void mv_run3(int nitems, int iters, int nc, UnitFn& unit, EpiFn& epi, const XS& xs,
+                                        int lane, MvBuf<FMT, R, U>& b0, MvBuf<FMT, R, U>& b1, DevMat N0, DevMat N1,
+                                        uint32_t nr0, uint32_t nrmax) {
+  MvBuf<FMT, R, U> b2;
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.f;
+  auto col = [&](int i) { return (i % iters) * U * TALOS_WAVE; };
+  auto ld = [&](MvBuf<FMT, R, U>& b, int i) {  // items are issued in order, so the unit changes at i % iters == 0
+    if (i % iters == 0) unit(i / iters, N0, N1, nr0, nrmax);
+    mv_load<FMT, R, U, PAIR>(b, N0, N1, nr0, nrmax, col(i), lane);
+  };
+  auto step = [&](const MvBuf<FMT, R, U>& b, int i) {
+    mv_compute<FMT, R, U>(b, xs, nc, col(i), lane, acc);
+    if (i % iters == iters - 1) {
+      float y[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        y[r] = wave_sum(acc[r]);
+        acc[r] = 0.f;
+      }
+      epi(i / iters, y);
+    }
+  };
+  int i = 0;
+  for (; i + 4 < nitems; i += 3) {  // items i+2, i+3 and i+4 exist
+    ld(b2, i + 2);
+    step(b0, i);
+    ld(b0, i + 3);
+    step(b1, i + 1);
+    ld(b1, i + 4);
+    step(b2, i + 2);
+  }
+  const int left = nitems - i;  // 0..4; b0 = item i, b1 = item i+1 when they exist
+  if (left == 4) {
+    ld(b2, i + 2);
+    step(b0, i);
+    ld(b0, i + 3);
+    step(b1, i + 1);
+    step(b2, i + 2);
+    step(b0, i + 3);
+  } else if (left == 3) {
+    ld(b2, i + 2);
+    step(b0, i);
+    step(b1, i + 1);
+    step(b2, i + 2);
+  } else if (left == 2) {
+    step(b0, i);
+    step(b1, i + 1);
+  } else if (left == 1) {
+    step(b0, i);
   }
 }
 
