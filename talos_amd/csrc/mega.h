@@ -341,7 +341,9 @@ __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t
 // positions (ng = 1, nsp = 1): no slice merge, and the group's K/V rows,
 // read by the group's items on one XCD, come from its L2.
 #define MEGA_ATTN_HG 4
+#ifndef MEGA_ATTN_STEP
 #define MEGA_ATTN_STEP 4
+#endif
 
 // Positions per slice: ceil(seq * n_kv / nblocks) rounded up to 16 (at
 // least 16), so that the items (KV head x slice) cover about one per block.

@@ -57,9 +57,6 @@ __device__ __forceinline__ XQ carve_xq(float* smem, int n, int gpb_max, int nwav
   return X;
 }
 
-// Round-to-nearest-even integer of t (|t| <= 127.5) and its byte.
-__device__ __forceinline__ float rne(float t) { return __builtin_rintf(t); }
-
 // Stage x (n floats, n % 32 == 0, n <= NR*512*8) as int8 planes, optionally
 // as rmsnorm(x)*w (src/math/ops.rs:5-12).  Thread t owns 8 consecutive
 // elements per round (4 threads = one block).  The loads of the parts of x
@@ -150,34 +147,43 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
     am = fmaxf(am, dpp_f<DPP_QUAD_2301>(am, am));
     const float inv = am > 0.f ? 127.f / am : 0.f;
     uint32_t pa[2], pb[2], pc[2];
-    float sa = 0.f, sb = 0.f, sc = 0.f;  // plane sums: integers below 2^12, exact
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      // t - a is exact, so fma(t, 254, -254 a) is (t - a) * 254 rounded
-      // once; each integer piece goes in as the biased byte piece + 128
-      // (v_cvt_pk_u8_f32 of an exact integer), unbiased by one xor per word.
-      uint32_t wa = 0, wb = 0, wc = 0;
+#pragma clang fp contract(off)
+      // r = t + 1.5 * 2^23 (|t| <= 127.5) rounds t to the nearest integer
+      // (ties to even) and holds it, two's complement, in r's low byte;
+      // -254 * (r - 1.5 * 2^23) = fma(r, -254, 254 * 1.5 * 2^23) exactly.
+      // t - a is exact, so fma(t, 254, -254 a) is (t - a) * 254 rounded once.
+      constexpr float kM = 12582912.f, k254M = 254.f * 12582912.f;
+      uint32_t ra[4], rb[4], rc[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float t = x[hh * 4 + k] * inv;
-        const float a = rne(t);
-        const float t2 = __builtin_fmaf(t, 254.f, -254.f * a);
-        const float b = rne(t2);
-        const float c = rne(__builtin_fmaf(t2, 254.f, -254.f * b));
-        sa += a;
-        sb += b;
-        sc += c;
-        wa = __builtin_amdgcn_cvt_pk_u8_f32(a + 128.f, k, wa);
-        wb = __builtin_amdgcn_cvt_pk_u8_f32(b + 128.f, k, wb);
-        wc = __builtin_amdgcn_cvt_pk_u8_f32(c + 128.f, k, wc);
+        const float fa = t + kM;
+        const float t2 = __builtin_fmaf(t, 254.f, __builtin_fmaf(fa, -254.f, k254M));
+        const float fb = t2 + kM;
+        const float fc = __builtin_fmaf(t2, 254.f, __builtin_fmaf(fb, -254.f, k254M)) + kM;
+        ra[k] = __float_as_uint(fa);
+        rb[k] = __float_as_uint(fb);
+        rc[k] = __float_as_uint(fc);
       }
-      pa[hh] = wa ^ 0x80808080u;
-      pb[hh] = wb ^ 0x80808080u;
-      pc[hh] = wc ^ 0x80808080u;
+      // low bytes of four words into one (v_perm_b32: 0-3 pick the second
+      // operand's bytes, 4-7 the first's, 0x0c gives 0)
+      auto pack = [](const uint32_t (&r)[4]) {
+        const uint32_t lo = __builtin_amdgcn_perm(r[1], r[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(r[3], r[2], 0x0c0c0400u);
+        return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      };
+      pa[hh] = pack(ra);
+      pb[hh] = pack(rb);
+      pc[hh] = pack(rc);
     }
-    sa = quad_sum(sa);
-    sb = quad_sum(sb);
-    sc = quad_sum(sc);
+    // plane sums over the block: integers below 2^12, exact in f32
+    auto bsum = [](const uint32_t (&p)[2]) {
+      return (float)__builtin_amdgcn_sdot4((int)p[0], 0x01010101, __builtin_amdgcn_sdot4((int)p[1], 0x01010101, 0,
+                                                                                             false), false);
+    };
+    const float sa = quad_sum(bsum(pa)), sb = quad_sum(bsum(pb)), sc = quad_sum(bsum(pc));
     if (ok) {
       const int blk = g8 >> 2, off = (g8 & 3) * 8;
       const size_t plane = (size_t)X.nb * 32;

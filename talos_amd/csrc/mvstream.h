@@ -311,7 +311,7 @@ __device__ __forceinline__ void mv_run3(int nitems, int iters, int nc, UnitFn& u
 // (nchunk <= U * 64), so a lane's x is the same for every item and is read
 // from LDS once, into registers.
 // DEPTH: items in flight, 2 (compute item i while item i+1 loads) or 3
-// (items i+1 and i+2 load; the first two are issued at pf).
+// (items i+1 and i+2 load while item i computes).
 template <uint32_t FMT, int R, int U, bool PAIR, bool XREG = false, int DEPTH = 2, class UnitFn, class ArriveFn,
           class StageFn, class EpiFn, class XS>
 __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arrive, StageFn stage, EpiFn epi,
@@ -334,23 +334,22 @@ __device__ __forceinline__ void mv_stream(int nunits, UnitFn unit, ArriveFn arri
   }
   arrive();
   const int nitems = nunits > 0 ? nunits * iters : 0;
-  // DEPTH 3: item 1 (item 0 again when there is no second item) goes into
-  // b1 with item 0, so both loads are unconditional.
-  DevMat N0 = A0, N1 = A1;
-  uint32_t nr0 = r0, nrmax = rmax;
-  auto pf = [&] {
-    mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane);
-    if constexpr (DEPTH == 3) {
-      const bool two = nitems > 1;
-      if (two && iters == 1) unit(1, N0, N1, nr0, nrmax);
-      mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, two && iters > 1 ? U * TALOS_WAVE : 0, lane);
-    }
-  };
+  auto pf = [&] { mv_load<FMT, R, U, PAIR>(b0, A0, A1, r0, rmax, 0, lane); };
   if (pre) {
     stage(pf);
   } else {
     stage([] {});
     pf();
+  }
+  // DEPTH 3: item 1 (item 0 again when there is no second item) goes into
+  // b1 unconditionally, after the staging: issued with item 0 its loads
+  // slow the staging's own reads of x more than they gain.
+  DevMat N0 = A0, N1 = A1;
+  uint32_t nr0 = r0, nrmax = rmax;
+  if constexpr (DEPTH == 3) {
+    const bool two = nitems > 1;
+    if (two && iters == 1) unit(1, N0, N1, nr0, nrmax);
+    mv_load<FMT, R, U, PAIR>(b1, N0, N1, nr0, nrmax, two && iters > 1 ? U * TALOS_WAVE : 0, lane);
   }
   if constexpr (XREG) {
     XIreg<U> xr;
