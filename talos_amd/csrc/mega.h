@@ -317,6 +317,16 @@ struct EmbSrc {
   }
 };
 
+// silu(g) * u (src/math/ops.rs:28-37) with exp2 and the reciprocal on the
+// transcendental unit: a few ulp from g / (1 + expf(-g)) * u, in 5 VALU
+// instructions instead of ~20 (an epilogue every gate/up item pays).
+// g -> -inf: 1 + exp2(+inf) = inf, rcp -> 0, the result -0 * u as with the
+// division.
+__device__ __forceinline__ float mega_swiglu(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 // Strided unit count for global wave gw of tw.
 __device__ __forceinline__ int mega_nunits(uint32_t total, uint32_t gw, uint32_t tw) {
   return gw < total ? (int)((total - gw + tw - 1) / tw) : 0;
@@ -886,7 +896,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 6);
       };
       auto fin = [&](int gi, int jj, float g, float u) {
-        st_coh(h + (size_t)gi * 8 + jj, (g / (1.0f + expf(-g))) * u);
+        st_coh(h + (size_t)gi * 8 + jj, mega_swiglu(g, u));
       };
       mq_phase<mq_item_tiles(UN * MEGA_NW), UN * MEGA_NW, 1, true, MEGA_NW>(ngr, gpb, grp, arrive, stage, fin, X, lane, wave);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
@@ -917,7 +927,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         for (int r = 0; r < PR; ++r) {
           if (p0 + r < P.ff) {
             const float g = y[2 * r], u = y[2 * r + 1];
-            st_coh(h + p0 + r, (g / (1.0f + expf(-g))) * u);
+            st_coh(h + p0 + r, mega_swiglu(g, u));
           }
         }
       };
