@@ -52,7 +52,8 @@ struct MegaParams {
   uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
   uint32_t nsplit, max_chunk;
   int attn_direct;  // sequences up to this length: one attention item per q head
-  int dsplit;       // down-projection in MEGA_DSPLIT column parts (int8-plane x)
+  int dsplit;       // down-projection in MEGA_DSPLIT column parts (int8-plane x): 1 the
+                    // parts on the waves of a team, 2 on different workgroups
   int embed;   // 1: x = embedding row of the state token, looked up on the device
   int hidden_only;
   int argmax;  // 0: none, 1: argmax into state, 2: + greedy advance, 3: + feed advance (advance_state)
@@ -78,10 +79,13 @@ __device__ __forceinline__ DevMat const_mat(const TALOS_CONST DevMat* p) {
 // Activation slots of one layer.  Every slot is written once per launch and
 // read only after the barrier that follows the write, so consumers read it
 // with ordinary cached loads (coherent.h).
-enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 3, MEGA_ACT_ATTY = 4, MEGA_ACT_H = 5 };
+// The down-projection output takes four slots (D..D+3): its column-quarter
+// sums when the quarters run on different workgroups (MegaParams::dsplit 2),
+// else the sum in slot D.
+enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 6, MEGA_ACT_ATTY = 7, MEGA_ACT_H = 8 };
 static inline __host__ __device__ uint32_t mega_np(uint32_t n) { return (n + 63) & ~63u; }
 static inline __host__ __device__ uint32_t mega_lstride(uint32_t n, uint32_t ff) {
-  return 5 * mega_np(n) + mega_np(ff);
+  return 8 * mega_np(n) + mega_np(ff);
 }
 __device__ __forceinline__ float* mega_act(const MegaParams& P, uint32_t l, int slot) {
   return P.act + (size_t)l * P.lstride + (size_t)slot * P.np;
@@ -308,6 +312,23 @@ struct Src3 {  // base and o-projection (final early) + the down-projection
   }
 };
 
+// base and o-projection (final early) + the four column-quarter sums of the
+// down-projection, added in quarter order first (as the sum of one
+// workgroup's quarters would be)
+struct Src6 {
+  static constexpr int kParts = 6, kEarly = 2;
+  const float *a, *b, *c;
+  uint32_t np;  // slot stride of the quarter sums
+  __device__ __forceinline__ f4 part(int s, int e) const {
+    return gld4((s == 0 ? a : (s == 1 ? b : c + (size_t)(s - 2) * np)) + e);
+  }
+  __device__ __forceinline__ static f4 sum(const f4* p) {
+    const f4 d{((p[2].x + p[3].x) + p[4].x) + p[5].x, ((p[2].y + p[3].y) + p[4].y) + p[5].y,
+               ((p[2].z + p[3].z) + p[4].z) + p[5].z, ((p[2].w + p[3].w) + p[4].w) + p[5].w};
+    return f4{(p[0].x + p[1].x) + d.x, (p[0].y + p[1].y) + d.y, (p[0].z + p[1].z) + d.z, (p[0].w + p[1].w) + d.w};
+  }
+};
+
 struct EmbSrc {
   static constexpr int kParts = 0, kEarly = 0;
   DevMat M;
@@ -325,6 +346,13 @@ struct EmbSrc {
 __device__ __forceinline__ float mega_swiglu(float g, float u) {
   const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
   return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
+// Element i of a layer's down-projection output (slots D..D+3 when its
+// column quarters ran on different workgroups).
+__device__ __forceinline__ float mega_down(const MegaParams& P, const float* d, uint32_t i) {
+  if (P.dsplit != 2) return gld(d + i);
+  return ((gld(d + i) + gld(d + P.np + i)) + gld(d + 2 * (size_t)P.np + i)) + gld(d + 3 * (size_t)P.np + i);
 }
 
 // Strided unit count for global wave gw of tw.
@@ -754,11 +782,17 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       auto stage = [&](auto&& pf) {
         if (l > 0) {
           // x = (base + attproj) + down of the previous layer; publish it
-          Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [&] {
+          auto w = [&] {
             wait();
             MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
-          });
+          };
+          if (P.dsplit == 2) {
+            Src6 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D), P.np};
+            X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
+          } else {
+            Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
+            X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
+          }
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
           X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [] {});
@@ -993,7 +1027,45 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
                                      pre);
             };
       if constexpr (IQ) {
-        if (P.dsplit) {
+        if (P.dsplit == 2) {
+          // The down rows in column quarters on different workgroups: block
+          // b takes quarter b % 4 of the columns of rows [(b / 4) * rpb, +rpb),
+          // rpb / 8 rows per wave in two-row units, and stages only its
+          // quarter of x (a quarter of the loads and the conversion); the
+          // quarter sums go to four slots that the next staging adds in
+          // quarter order.
+          constexpr int KS = MEGA_DSPLIT, RD = 2;
+          const uint32_t part = blockIdx.x % KS, grp = blockIdx.x / KS;
+          const uint32_t qn = LP->d.nchunk / KS;  // chunks per quarter
+          const uint32_t rpb = P.n / (nb / KS), rpw = rpb / MEGA_NW;
+          const MegaX<IQ> X(smem, (int)qn * 32, need_l);
+          const uint32_t row0 = grp * rpb + (uint32_t)wave * rpw;
+          auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
+            A0 = const_mat(&LP->d);
+            A0.q += (size_t)part * qn * fmt_chunk_qbytes(LF);
+            A0.d += (size_t)part * qn;
+            A0.nchunk = qn;
+            A1 = A0;
+            r0 = row0 + (uint32_t)k * RD;
+            rmax = LP->d.rows;
+          };
+          auto stage = [&](auto&& pf) {
+            Src1 src{h + (size_t)part * qn * 32};
+            X.stage(src, (int)qn * 32, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
+              wait();
+              MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
+            });
+            MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
+          };
+          float* dq = d_out + (size_t)part * P.np;
+          auto epi = [&](int k, const float(&y)[RD]) {
+            if (lane != 0) return;
+#pragma unroll
+            for (int r = 0; r < RD; ++r) st_coh(dq + row0 + (uint32_t)k * RD + r, y[r]);
+          };
+          constexpr int DD = LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_D : 2;
+          mv_stream<LF, RD, UN, false, true, DD>((int)(rpw / RD), unit, arrive, stage, epi, X.src(LL), lane, pre);
+        } else if (P.dsplit) {
           // The down rows in column quarters: the four waves of a team (waves
           // 4t..4t+3 of a block) each take one quarter of the columns of the
           // team's rows, two rows per unit, with the x of their quarter held in
@@ -1061,13 +1133,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     if (blockIdx.x == 0) {
       float ss = 0.f;
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (gld(last + i) + gld(last_o + i)) + gld(last_d + i);
+        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, last_d, i);
         ss += v * v;
       }
       ss = block_sum(ss, smem, MEGA_NW);
       const float scale = 1.0f / sqrtf(ss / (float)P.n + P.eps);
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (gld(last + i) + gld(last_o + i)) + gld(last_d + i);
+        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, last_d, i);
         P.hidden[i] = v * scale * P.out_norm[i];
       }
     }
@@ -1081,8 +1153,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       rmax = P.out_w.rows;
     };
     auto stage = [&](auto&& pf) {
-      Src3 src{last, last_o, last_d};
-      X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
+      if (P.dsplit == 2) {
+        Src6 src{last, last_o, last_d, P.np};
+        X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
+      } else {
+        Src3 src{last, last_o, last_d};
+        X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
+      }
       MEGA_MARK(P, P.n_layer * MEGA_TL_PER_LAYER + 0);
     };
     auto epi = [&](int k, const float(&y)[RO]) {

@@ -111,8 +111,9 @@ struct talos_hip_ctx {
   // TALOS_HIP_ATTN_DIRECT: longest sequence whose attention runs one item
   // per q head with no slice merge (0: always slices).
   int attn_direct = 256;
-  // TALOS_HIP_DSPLIT=0 keeps the down-projection rows whole.
-  bool allow_dsplit = true;
+  // TALOS_HIP_DSPLIT=0 keeps the down-projection rows whole, =1 splits their
+  // columns over the waves of a workgroup only (default: over workgroups).
+  int allow_dsplit = 2;
   int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
   MegaParams mp{};
 };
@@ -706,9 +707,16 @@ int mega_setup(talos_hip_ctx* c) {
     // item, and an even number of rows per team of MEGA_DSPLIT waves
     const uint32_t teams = c->mega_blocks * (MEGA_NW / MEGA_DSPLIT), dch = cf.n_ff / 32;
     const uint32_t rpt = cf.n_embd / teams;
-    P.dsplit = c->mega_mode == MEGA_MM_DOT4 && c->allow_dsplit && dch % MEGA_DSPLIT == 0 &&
-               dch / MEGA_DSPLIT <= (uint32_t)mv_u(cf.n_embd / 32) * 64 && rpt * teams == cf.n_embd &&
-               rpt % 2 == 0 && rpt <= MEGA_DSPLIT_ROWS && rpt * (MEGA_NW / MEGA_DSPLIT) <= MEGA_NT;
+    const bool quarters = c->mega_mode == MEGA_MM_DOT4 && c->allow_dsplit > 0 && dch % MEGA_DSPLIT == 0 &&
+                          dch / MEGA_DSPLIT <= (uint32_t)mv_u(cf.n_embd / 32) * 64;
+    P.dsplit = quarters && rpt * teams == cf.n_embd && rpt % 2 == 0 && rpt <= MEGA_DSPLIT_ROWS &&
+               rpt * (MEGA_NW / MEGA_DSPLIT) <= MEGA_NT;
+    // the quarters on different workgroups: whole groups of four blocks, an
+    // even number of rows per wave
+    const uint32_t groups = c->mega_blocks / MEGA_DSPLIT;
+    if (quarters && c->allow_dsplit == 2 && c->mega_blocks % MEGA_DSPLIT == 0 && cf.n_embd % groups == 0 &&
+        (cf.n_embd / groups) % (2 * MEGA_NW) == 0)
+      P.dsplit = 2;
   }
   c->mega_fn = fn;
   c->mega_ready = true;
@@ -797,7 +805,7 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   env = getenv("TALOS_HIP_DOT4");
   c->allow_dot4 = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_DSPLIT");
-  c->allow_dsplit = !(env && env[0] == '0');
+  c->allow_dsplit = env && (env[0] == '0' || env[0] == '1') ? env[0] - '0' : 2;
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
