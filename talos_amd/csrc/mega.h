@@ -79,16 +79,28 @@ __device__ __forceinline__ DevMat const_mat(const TALOS_CONST DevMat* p) {
 // Activation slots of one layer.  Every slot is written once per launch and
 // read only after the barrier that follows the write, so consumers read it
 // with ordinary cached loads (coherent.h).
-// The down-projection output takes four slots (D..D+3): its column-quarter
-// sums when the quarters run on different workgroups (MegaParams::dsplit 2),
-// else the sum in slot D.
-enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 6, MEGA_ACT_ATTY = 7, MEGA_ACT_H = 8 };
+// The down-projection output is slot D, or, when its column quarters run on
+// different workgroups (MegaParams::dsplit 2), the quarter sums: quarter 0
+// in slot D, quarters 1..3 in three slots per layer after the last layer's
+// (the layer stride, and so the placement of the other slots, stays that of
+// five slots and h: measured, a longer stride slowed the attention phase's
+// q reads and output stores by ~4 us per layer).
+enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 3, MEGA_ACT_ATTY = 4, MEGA_ACT_H = 5 };
 static inline __host__ __device__ uint32_t mega_np(uint32_t n) { return (n + 63) & ~63u; }
 static inline __host__ __device__ uint32_t mega_lstride(uint32_t n, uint32_t ff) {
-  return 8 * mega_np(n) + mega_np(ff);
+  return 5 * mega_np(n) + mega_np(ff);
+}
+// floats of the activation area: n_layer strides, then the quarter slots
+static inline __host__ __device__ size_t mega_act_floats(uint32_t n_layer, uint32_t n, uint32_t ff) {
+  return (size_t)n_layer * (mega_lstride(n, ff) + 3 * mega_np(n));
 }
 __device__ __forceinline__ float* mega_act(const MegaParams& P, uint32_t l, int slot) {
   return P.act + (size_t)l * P.lstride + (size_t)slot * P.np;
+}
+// quarter q's slot of layer l's down-projection sums
+__device__ __forceinline__ float* mega_dq(const MegaParams& P, uint32_t l, uint32_t q) {
+  return q == 0 ? mega_act(P, l, MEGA_ACT_D)
+                : P.act + (size_t)P.n_layer * P.lstride + ((size_t)l * 3 + q - 1) * P.np;
 }
 // Residual base of layer l: the host-supplied x for layer 0 unless the
 // embedding is looked up on the device.
@@ -165,11 +177,13 @@ __device__ __forceinline__ void mega_stage_v(Src src, int n, const float* __rest
     const int e4 = i * MEGA_NT + tid;
     src_load_late(src, (e4 < nr ? e4 : nr - 1) * 4, raw[i]);
   }
+  constexpr bool kSumFirst = Src::kParts >= 5;  // as in stage_xq
   __builtin_amdgcn_sched_barrier(0);
-  after();
+  if constexpr (!kSumFirst) after();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i) v[i] = src_sum<Src>(raw[i]);
+  if constexpr (kSumFirst) after();
 #pragma unroll
   for (int i = 0; i < MEGA_VPT; ++i)
     if (i * MEGA_NT + tid >= nr) v[i] = f4{0.f, 0.f, 0.f, 0.f};
@@ -229,6 +243,11 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
 #endif
 #ifndef MEGA_DEPTH_D
 #define MEGA_DEPTH_D 2
+#endif
+// ... and in the down-projection with its quarters on different workgroups
+// (four units per wave, each block staging only its quarter)
+#ifndef MEGA_DEPTH_DQ
+#define MEGA_DEPTH_DQ 3
 #endif
 
 // stage_xq with the fewest rounds of 8 elements per thread covering n.
@@ -312,20 +331,24 @@ struct Src3 {  // base and o-projection (final early) + the down-projection
   }
 };
 
-// base and o-projection (final early) + the four column-quarter sums of the
+// base + o-projection (final early, added as they are loaded: fewer
+// registers held across the barrier) + the four column-quarter sums of the
 // down-projection, added in quarter order first (as the sum of one
 // workgroup's quarters would be)
 struct Src6 {
-  static constexpr int kParts = 6, kEarly = 2;
-  const float *a, *b, *c;
-  uint32_t np;  // slot stride of the quarter sums
+  static constexpr int kParts = 5, kEarly = 1;
+  const float *a, *b, *c0, *c1, *c2, *c3;
   __device__ __forceinline__ f4 part(int s, int e) const {
-    return gld4((s == 0 ? a : (s == 1 ? b : c + (size_t)(s - 2) * np)) + e);
+    if (s == 0) {
+      const f4 x = gld4(a + e), y = gld4(b + e);
+      return f4{x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+    }
+    return gld4((s == 1 ? c0 : s == 2 ? c1 : s == 3 ? c2 : c3) + e);
   }
   __device__ __forceinline__ static f4 sum(const f4* p) {
-    const f4 d{((p[2].x + p[3].x) + p[4].x) + p[5].x, ((p[2].y + p[3].y) + p[4].y) + p[5].y,
-               ((p[2].z + p[3].z) + p[4].z) + p[5].z, ((p[2].w + p[3].w) + p[4].w) + p[5].w};
-    return f4{(p[0].x + p[1].x) + d.x, (p[0].y + p[1].y) + d.y, (p[0].z + p[1].z) + d.z, (p[0].w + p[1].w) + d.w};
+    const f4 d{((p[1].x + p[2].x) + p[3].x) + p[4].x, ((p[1].y + p[2].y) + p[3].y) + p[4].y,
+               ((p[1].z + p[2].z) + p[3].z) + p[4].z, ((p[1].w + p[2].w) + p[3].w) + p[4].w};
+    return f4{p[0].x + d.x, p[0].y + d.y, p[0].z + d.z, p[0].w + d.w};
   }
 };
 
@@ -350,9 +373,10 @@ __device__ __forceinline__ float mega_swiglu(float g, float u) {
 
 // Element i of a layer's down-projection output (slots D..D+3 when its
 // column quarters ran on different workgroups).
-__device__ __forceinline__ float mega_down(const MegaParams& P, const float* d, uint32_t i) {
-  if (P.dsplit != 2) return gld(d + i);
-  return ((gld(d + i) + gld(d + P.np + i)) + gld(d + 2 * (size_t)P.np + i)) + gld(d + 3 * (size_t)P.np + i);
+__device__ __forceinline__ float mega_down(const MegaParams& P, uint32_t l, uint32_t i) {
+  if (P.dsplit != 2) return gld(mega_act(P, l, MEGA_ACT_D) + i);
+  return ((gld(mega_dq(P, l, 0) + i) + gld(mega_dq(P, l, 1) + i)) + gld(mega_dq(P, l, 2) + i)) +
+         gld(mega_dq(P, l, 3) + i);
 }
 
 // Strided unit count for global wave gw of tw.
@@ -786,10 +810,16 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             wait();
             MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 0);
           };
-          if (P.dsplit == 2) {
-            Src6 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D), P.np};
-            X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
-          } else {
+          bool done = false;
+          if constexpr (IQ) {  // quarter sums: int8-plane kernels only
+            if (P.dsplit == 2) {
+              Src6 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_dq(P, l - 1, 0),
+                       mega_dq(P, l - 1, 1),   mega_dq(P, l - 1, 2),              mega_dq(P, l - 1, 3)};
+              X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
+              done = true;
+            }
+          }
+          if (!done) {
             Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
             X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
           }
@@ -1057,13 +1087,14 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             });
             MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
           };
-          float* dq = d_out + (size_t)part * P.np;
+          float* dq = mega_dq(P, l, part);
           auto epi = [&](int k, const float(&y)[RD]) {
             if (lane != 0) return;
-#pragma unroll
-            for (int r = 0; r < RD; ++r) st_coh(dq + row0 + (uint32_t)k * RD + r, y[r]);
+            const uint64_t v2 = (uint64_t)__float_as_uint(y[0]) | ((uint64_t)__float_as_uint(y[1]) << 32);
+            __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(dq + row0 + (uint32_t)k * RD)), v2, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);  // the unit's two rows in one store
           };
-          constexpr int DD = LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_D : 2;
+          constexpr int DD = LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_DQ : 2;
           mv_stream<LF, RD, UN, false, true, DD>((int)(rpw / RD), unit, arrive, stage, epi, X.src(LL), lane, pre);
         } else if (P.dsplit) {
           // The down rows in column quarters: the four waves of a team (waves
@@ -1133,13 +1164,13 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     if (blockIdx.x == 0) {
       float ss = 0.f;
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, last_d, i);
+        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, ll, i);
         ss += v * v;
       }
       ss = block_sum(ss, smem, MEGA_NW);
       const float scale = 1.0f / sqrtf(ss / (float)P.n + P.eps);
       for (uint32_t i = threadIdx.x; i < P.n; i += MEGA_NT) {
-        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, last_d, i);
+        const float v = (gld(last + i) + gld(last_o + i)) + mega_down(P, ll, i);
         P.hidden[i] = v * scale * P.out_norm[i];
       }
     }
@@ -1153,10 +1184,15 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       rmax = P.out_w.rows;
     };
     auto stage = [&](auto&& pf) {
-      if (P.dsplit == 2) {
-        Src6 src{last, last_o, last_d, P.np};
-        X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
-      } else {
+      bool done = false;
+      if constexpr (IQ) {
+        if (P.dsplit == 2) {
+          Src6 src{last, last_o, mega_dq(P, ll, 0), mega_dq(P, ll, 1), mega_dq(P, ll, 2), mega_dq(P, ll, 3)};
+          X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
+          done = true;
+        }
+      }
+      if (!done) {
         Src3 src{last, last_o, last_d};
         X.stage(src, P.n, P.out_norm, P.eps, true, nullptr, 0, 0, pf, [&] { wait(); });
       }

@@ -101,14 +101,19 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
     src_load_late(src, gg * 8, raw[r][0]);
     src_load_late(src, gg * 8 + 4, raw[r][1]);
   }
+  // A source of many parts (Src6) takes its sums before the first weight
+  // loads are issued: its loads and those loads would not fit the registers
+  // together.
+  constexpr bool kSumFirst = Src::kParts >= 5;
   __builtin_amdgcn_sched_barrier(0);
-  after();
+  if constexpr (!kSumFirst) after();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     v[r][0] = src_sum<Src>(raw[r][0]);
     v[r][1] = src_sum<Src>(raw[r][1]);
   }
+  if constexpr (kSumFirst) after();
 #pragma unroll
   for (int r = 0; r < NR; ++r)
     if (r * NT + tid >= n8) v[r][0] = v[r][1] = f4{0.f, 0.f, 0.f, 0.f};

@@ -662,7 +662,7 @@ int mega_setup(talos_hip_ctx* c) {
   HIPCHK(c, hipMemcpy(c->d_layers, L.data(), sizeof(MegaLayer) * cf.n_layer, hipMemcpyHostToDevice));
   const uint32_t lstride = mega_lstride(cf.n_embd, cf.n_ff);
   const size_t pstride = (size_t)cf.n_head_kv * msplit * c->group * (c->hd + 2);
-  if (!c->mact) HIPCHK(c, hipMalloc(&c->mact, (size_t)cf.n_layer * lstride * 4));
+  if (!c->mact) HIPCHK(c, hipMalloc(&c->mact, mega_act_floats(cf.n_layer, cf.n_embd, cf.n_ff) * 4));
   if (!c->mpart) HIPCHK(c, hipMalloc(&c->mpart, (size_t)cf.n_layer * pstride * 4));
   if (!c->d_sync) {
     const size_t words = mega_sync_words(c->mega_blocks);
