@@ -82,9 +82,7 @@ __device__ __forceinline__ DevMat const_mat(const TALOS_CONST DevMat* p) {
 // The down-projection output is slot D, or, when its column quarters run on
 // different workgroups (MegaParams::dsplit 2), the quarter sums: quarter 0
 // in slot D, quarters 1..3 in three slots per layer after the last layer's
-// (the layer stride, and so the placement of the other slots, stays that of
-// five slots and h: measured, a longer stride slowed the attention phase's
-// q reads and output stores by ~4 us per layer).
+// (the layer stride stays that of five slots and h).
 enum { MEGA_ACT_BASE = 0, MEGA_ACT_O = 1, MEGA_ACT_D = 2, MEGA_ACT_Q = 3, MEGA_ACT_ATTY = 4, MEGA_ACT_H = 5 };
 static inline __host__ __device__ uint32_t mega_np(uint32_t n) { return (n + 63) & ~63u; }
 static inline __host__ __device__ uint32_t mega_lstride(uint32_t n, uint32_t ff) {
