@@ -52,6 +52,7 @@ struct MegaParams {
   uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
   uint32_t nsplit, max_chunk;
   int attn_direct;  // sequences up to this length: one attention item per q head
+  int attn_wait;    // attention blocks wait for their q/k/v producers only, not a grid barrier
   int dsplit;       // down-projection in MEGA_DSPLIT column parts (int8-plane x): 1 the
                     // parts on the waves of a team, 2 on different workgroups
   int embed;   // 1: x = embedding row of the state token, looked up on the device
@@ -861,8 +862,6 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
     }
     // ---- attention over positions 0..pos
     {
-      grid_barrier(G, ++ep);
-      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 2);
       // slices of >= 16 positions, sized so that the items (KV head x
       // slice) cover about one per block
       const int seq = pos + 1;
@@ -872,10 +871,41 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       // b % n_kv (a group's items sit on blocks congruent mod n_kv), over
       // all positions; otherwise item b is slice b / n_kv of KV head b % n_kv
       const bool direct = seq <= P.attn_direct;
+      const uint32_t items = direct ? P.n_kv * P.group : P.n_kv * (uint32_t)nsp;
+      if (!MF && P.attn_wait) {
+        // Every block arrives; a block with attention items then waits only
+        // for the blocks that computed their q, k and v rows (qkv unit u
+        // runs on wave u % tw), the others go on to the o-projection's
+        // barrier.
+        grid_arrive(G, ep + 1);
+        ++ep;
+        __syncthreads();  // barrier_skip() as thread 0 read it
+        if (blockIdx.x < items && !barrier_skip()) {
+          for (uint32_t it = blockIdx.x; it < items; it += nb) {
+            const uint32_t jj = it % P.n_kv, hq0 = jj * P.group + (direct ? it / P.n_kv : 0);
+            const uint32_t ng = direct ? 1 : P.group, hu = P.hd / RL;  // units per head
+            const uint32_t nq = ng * hu, uq0 = hq0 * hu, uk0 = P.n / RL + jj * hu, uv0 = uk0 + P.kv_dim / RL;
+            for (uint32_t t = threadIdx.x; t < nq + 2 * hu; t += MEGA_NT) {
+              const uint32_t u = t < nq ? uq0 + t : (t < nq + hu ? uk0 + (t - nq) : uv0 + (t - nq - hu));
+              const uint32_t b = (u % tw) / MEGA_NW;
+              uint32_t k = 0;
+              while ((int32_t)(ld_coh_u(G.flags + b * 16) - ep) < 0) {
+                if (++k > TALOS_SPIN_LIMIT) {
+                  st_coh_u(G.err, 1u);
+                  break;
+                }
+              }
+            }
+          }
+        }
+        __syncthreads();
+      } else {
+        grid_barrier(G, ++ep);
+      }
+      MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 2);
       if (!direct && nsp > (int)P.nsplit) {
         if (threadIdx.x == 0) st_coh_u(G.err, 1u);  // host sized the partials too small
       } else {
-        const uint32_t items = direct ? P.n_kv * P.group : P.n_kv * (uint32_t)nsp;
         float* part = P.part + (size_t)l * P.pstride;
         for (uint32_t it = blockIdx.x; it < items; it += nb) {
           const uint32_t jj = it % P.n_kv, r = it / P.n_kv;

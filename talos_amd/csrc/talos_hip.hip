@@ -114,6 +114,8 @@ struct talos_hip_ctx {
   // TALOS_HIP_DSPLIT=0 keeps the down-projection rows whole, =1 splits their
   // columns over the waves of a workgroup only (default: over workgroups).
   int allow_dsplit = 2;
+  // TALOS_HIP_ATTN_WAIT=0 keeps a grid barrier in front of the attention.
+  bool allow_attn_wait = true;
   int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
   MegaParams mp{};
 };
@@ -702,6 +704,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.nsplit = msplit;
   P.max_chunk = MEGA_ATTN_STEP;
   P.attn_direct = c->attn_direct;
+  P.attn_wait = c->allow_attn_wait ? 1 : 0;
   {
     // split down-projection: whole quarters of the row chunks that fit one
     // item, and an even number of rows per team of MEGA_DSPLIT waves
@@ -804,6 +807,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_mfma = env && env[0] == '1';
   env = getenv("TALOS_HIP_DOT4");
   c->allow_dot4 = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_ATTN_WAIT");
+  c->allow_attn_wait = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_DSPLIT");
   c->allow_dsplit = env && (env[0] == '0' || env[0] == '1') ? env[0] - '0' : 2;
   env = getenv("TALOS_HIP_ATTN_DIRECT");
