@@ -861,6 +861,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 1);
     }
     // ---- attention over positions 0..pos
+    uint32_t o_prod = nb;  // the blocks [0, o_prod) write the attention output
     {
       // slices of >= 16 positions, sized so that the items (KV head x
       // slice) cover about one per block
@@ -872,6 +873,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       // all positions; otherwise item b is slice b / n_kv of KV head b % n_kv
       const bool direct = seq <= P.attn_direct;
       const uint32_t items = direct ? P.n_kv * P.group : P.n_kv * (uint32_t)nsp;
+      if (!MF && P.attn_wait && direct) o_prod = items < nb ? items : nb;
       if (!MF && P.attn_wait) {
         // Every block arrives; a block with attention items then waits only
         // for the blocks that computed their q, k and v rows (qkv unit u
@@ -955,7 +957,24 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       auto stage = [&](auto&& pf) {
         Src1 src{atty};
         X.stage(src, P.n, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
-          wait();
+          if (o_prod < nb) {
+            // short sequences: only the item blocks [0, o_prod) wrote the
+            // attention output; wait for their arrival flags directly
+            ++ep;
+            __syncthreads();
+            if (!barrier_skip() && threadIdx.x < o_prod) {
+              uint32_t k = 0;
+              while ((int32_t)(ld_coh_u(G.flags + threadIdx.x * 16) - ep) < 0) {
+                if (++k > TALOS_SPIN_LIMIT) {
+                  st_coh_u(G.err, 1u);
+                  break;
+                }
+              }
+            }
+            __syncthreads();
+          } else {
+            wait();
+          }
           MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 1);
         });
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 4);
