@@ -1,0 +1,49 @@
+"""The persistent kernel's synchronisation variants compute the same bits.
+
+At the 7B shape (Q4_0 layers, Q6_K output) the default decode step
+  * lets the attention items wait only for the blocks that produced their
+    q, k and v rows, and the o-projection staging (short sequences) only for
+    the attention item blocks, and
+  * runs the down-projection's column quarters on different workgroups, the
+    quarter sums added in quarter order by the next staging.
+TALOS_HIP_ATTN_WAIT=0 puts full grid barriers back; TALOS_HIP_DSPLIT=1
+splits the quarters over the waves of one workgroup, summed in the same
+order in LDS.  Neither changes an arithmetic operation or its order, so the
+logits and the cache must match the default bit for bit (the default path
+itself is checked against the oracle by the parity tests).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(talos, spec, prompt):
+    m = talos.Model.synth(spec, nthreads=16)
+    try:
+        m.reset()
+        out = []
+        for p, t in enumerate(prompt):
+            logits, am = m.forward_token(int(t), p)
+            out.append((logits.copy(), am))
+        k, v = m.kv_read(len(prompt))
+        return out, k, v
+    finally:
+        m.close()
+
+
+def test_sync_variants_bit_identical(talos, monkeypatch):
+    from talos_amd import configs
+    wl = configs.mistral7b_q4(ctx=256)
+    prompt = np.random.default_rng(wl.spec.seed + 11).integers(0, wl.spec.vocab_size, 6).astype(np.uint32)
+    print("\n[sync] default synchronisation", flush=True)
+    base, kb, vb = _run(talos, wl.spec, prompt)
+    monkeypatch.setenv("TALOS_HIP_ATTN_WAIT", "0")
+    monkeypatch.setenv("TALOS_HIP_DSPLIT", "1")
+    print("[sync] grid barriers, in-workgroup quarter split", flush=True)
+    alt, ka, va = _run(talos, wl.spec, prompt)
+    for i, ((a, am_a), (b, am_b)) in enumerate(zip(base, alt)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"pos {i}: logits differ"
+        assert am_a == am_b
+    assert np.array_equal(kb.view(np.uint32), ka.view(np.uint32))
+    assert np.array_equal(vb.view(np.uint32), va.view(np.uint32))
