@@ -706,6 +706,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   const uint32_t tok = (uint32_t)P.state[ST_TOKEN];
   const uint32_t half = P.hd / 2;
   constexpr int RL = mv_rows(LF), RO = mv_rows(OF);
+  // gate/up waves take contiguous runs of row pairs (int8-plane Q4_0 layers)
+  constexpr bool GU_RUNS = IQ && LF == TALOS_FMT_Q4_0;
   constexpr int LL = MvT<LF>::L, LO = MvT<OF>::L;
   const int need_l = 1 << LL, need_o = 1 << LO;
   // each matvec phase issues its first weight loads right behind its staging
@@ -1017,10 +1019,21 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       constexpr int RG = IQ ? 2 : RL, PR = RG / 2;
       const MegaX<IQ> X(smem, P.n, need_l);
       const uint32_t total = (P.ff + PR - 1) / PR;
+      // With the down rows' column quarters on different workgroups and
+      // producer-only waits, wave gw takes the contiguous run of pairs
+      // [gw * upw, +upw): a quarter of the SwiGLU output then comes from one
+      // contiguous range of blocks, which the down staging waits for alone.
+      // Q4_0 only: with Q8_0 rows the runs slow the gate/up streaming by
+      // more than the wait saves.
+      const bool gu_run = GU_RUNS && P.dsplit == 2 && P.attn_wait;
+      const uint32_t upw = (total + tw - 1) / tw;
+      auto pair0 = [&](int k) { return gu_run ? gw * upw + (uint32_t)k : gw + (uint32_t)k * tw; };
+      const int gu_units = gu_run ? (gw * upw < total ? (int)min(upw, total - gw * upw) : 0)
+                                  : mega_nunits(total, gw, tw);
       auto unit = [&](int k, DevMat& A0, DevMat& A1, uint32_t& r0, uint32_t& rmax) {
         A0 = const_mat(&LP->g);
         A1 = const_mat(&LP->u);
-        r0 = (gw + (uint32_t)k * tw) * PR;
+        r0 = pair0(k) * PR;
         rmax = LP->g.rows;
       };
       auto stage = [&](auto&& pf) {
@@ -1033,7 +1046,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       };
       auto epi = [&](int k, const float(&y)[RG]) {
         if (lane != 0) return;
-        const uint32_t p0 = (gw + (uint32_t)k * tw) * PR;
+        const uint32_t p0 = pair0(k) * PR;
 #pragma unroll
         for (int r = 0; r < PR; ++r) {
           if (p0 + r < P.ff) {
@@ -1043,8 +1056,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         }
       };
       constexpr int DG = IQ && LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_GU : 2;
-      mv_stream<LF, RG, UN, true, IQ, DG>(mega_nunits(total, gw, tw), unit, arrive, stage, epi, X.src(LL), lane,
-                                          pre);
+      mv_stream<LF, RG, UN, true, IQ, DG>(gu_units, unit, arrive, stage, epi, X.src(LL), lane, pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
     // ---- down-projection (2-row units keep the long rows' double buffer in
@@ -1129,7 +1141,29 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           auto stage = [&](auto&& pf) {
             Src1 src{h + (size_t)part * qn * 32};
             X.stage(src, (int)qn * 32, nullptr, 0.f, false, nullptr, 0, 0, pf, [&] {
-              wait();
+              if (GU_RUNS && P.attn_wait) {
+                // gate/up wave gw wrote the SwiGLU outputs [gw * upw, +upw):
+                // wait for the arrival flags of the blocks that wrote this
+                // quarter [e0, e1) only
+                ++ep;
+                __syncthreads();
+                const uint32_t upw = (P.ff + tw - 1) / tw, e0 = part * qn * 32, e1 = e0 + qn * 32;
+                const uint32_t b0 = e0 / upw / MEGA_NW, b1 = (e1 - 1) / upw / MEGA_NW;
+                if (!barrier_skip()) {
+                  for (uint32_t b = b0 + threadIdx.x; b <= b1 && b < nb; b += MEGA_NT) {
+                    uint32_t k = 0;
+                    while ((int32_t)(ld_coh_u(G.flags + b * 16) - ep) < 0) {
+                      if (++k > TALOS_SPIN_LIMIT) {
+                        st_coh_u(G.err, 1u);
+                        break;
+                      }
+                    }
+                  }
+                }
+                __syncthreads();
+              } else {
+                wait();
+              }
               MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 3);
             });
             MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 8);
