@@ -95,11 +95,14 @@ struct talos_hip_ctx {
   float* mact = nullptr;   // per-layer activation slots
   float* mpart = nullptr;  // per-layer attention slice partials
   bool mega_prefetch = true;  // TALOS_HIP_PREFETCH=0 turns cross-barrier weight prefetch off
-  // TALOS_HIP_COOP=0 launches the persistent kernel with an ordinary launch
-  // (same grid, one workgroup per CU), for tools that mishandle cooperative
-  // launches.  Co-residency is then not promised by the runtime; a barrier
-  // that cannot complete times out and the step reports an error.
-  bool mega_coop = true;
+  // The persistent kernel goes out as an ordinary launch: its grid is one
+  // workgroup per CU and the set-up's occupancy check admits it only when at
+  // least one fits per CU, so on an otherwise idle device every workgroup is resident
+  // at once; a workgroup held back by other work on the device makes the
+  // bounded barrier spins time out and the step report an error, never hang.
+  // TALOS_HIP_COOP=1 uses hipLaunchCooperativeKernel instead (the runtime
+  // then checks co-residency), which adds ~25 us per step on the MI355X.
+  bool mega_coop = false;
   // TALOS_HIP_MFMA=1 runs the Q4_0 layer matvecs of the persistent kernel on
   // the matrix cores (mfma.h; parity-tested, not yet faster than the vector
   // path, so off by default).
@@ -802,7 +805,7 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   env = getenv("TALOS_HIP_PREFETCH");
   c->mega_prefetch = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_COOP");
-  c->mega_coop = !(env && env[0] == '0');
+  c->mega_coop = env && env[0] == '1';
   env = getenv("TALOS_HIP_MFMA");
   c->allow_mfma = env && env[0] == '1';
   env = getenv("TALOS_HIP_DOT4");
