@@ -2,11 +2,14 @@
 
 At the 7B shape (Q4_0 layers, Q6_K output) the default decode step
   * lets the attention items wait only for the blocks that produced their
-    q, k and v rows, and the o-projection staging (short sequences) only for
-    the attention item blocks, and
+    q, k and v rows, the o-projection staging (short sequences) only for
+    the attention item blocks, and each down-projection column quarter only
+    for the blocks whose gate/up waves (contiguous runs of row pairs) wrote
+    its inputs, and
   * runs the down-projection's column quarters on different workgroups, the
     quarter sums added in quarter order by the next staging.
-TALOS_HIP_ATTN_WAIT=0 puts full grid barriers back; TALOS_HIP_DSPLIT=1
+TALOS_HIP_ATTN_WAIT=0 puts full grid barriers back (and the gate/up pairs
+strided over the waves); TALOS_HIP_DSPLIT=1
 splits the quarters over the waves of one workgroup, summed in the same
 order in LDS.  Neither changes an arithmetic operation or its order, so the
 logits and the cache must match the default bit for bit (the default path
