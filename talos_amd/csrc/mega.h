@@ -1,15 +1,17 @@
 // mega.h -- one persistent kernel per decode step.
 //
 // The whole token (src/model/llama.rs:96-183 plus the output projection and
-// the greedy argmax of src/sample.rs:7-14) runs in one cooperative launch of
-// one 512-thread workgroup per CU.  Phases per layer:
+// the greedy argmax of src/sample.rs:7-14) runs in one launch of one
+// 512-thread workgroup per CU (one fits per CU and the grid is the CU count,
+// so all are resident at once).  Phases per layer:
 //   qkv (rmsnorm + q/k/v + RoPE + K/V append) | attention | o + residual |
 //   rmsnorm + gate/up + SwiGLU | down + residual
 // then rmsnorm + output projection with a fused argmax.  A grid barrier
-// (coherent.h) separates dependent phases.  Each matvec phase issues its
-// first weight loads *before* waiting at the barrier that precedes it, so
-// HBM keeps streaming while the grid synchronizes.  Activations cross
-// workgroups only through coherent loads/stores.
+// (coherent.h), or a wait on the arrival flags of just the workgroups that
+// produced a phase's input, separates dependent phases.  A phase loads the
+// parts of its input that are final before the wait, waits, loads the rest,
+// and issues its first weight loads right behind those staging loads.
+// Activations cross workgroups only through coherent loads/stores.
 #pragma once
 #include "coherent.h"
 #include "kernels.h"
