@@ -70,3 +70,22 @@ def test_whole_down_rows_close(talos, monkeypatch):
         print(f"  pos {i}: max-abs logit diff {d:.3e}", flush=True)
         assert d <= 1e-3
         assert am_a == am_b
+
+
+def test_cooperative_launch_bit_identical(talos, monkeypatch):
+    """TALOS_HIP_COOP=1 sends the same persistent kernel and grid out through
+    hipLaunchCooperativeKernel instead of an ordinary launch: the logits and
+    the cache must not change by a bit."""
+    from talos_amd import configs
+    wl = configs.mistral7b_q4(ctx=256)
+    prompt = np.random.default_rng(wl.spec.seed + 13).integers(0, wl.spec.vocab_size, 4).astype(np.uint32)
+    print("\n[sync] ordinary launch", flush=True)
+    base, kb, vb = _run(talos, wl.spec, prompt)
+    monkeypatch.setenv("TALOS_HIP_COOP", "1")
+    print("[sync] cooperative launch", flush=True)
+    alt, ka, va = _run(talos, wl.spec, prompt)
+    for i, ((a, am_a), (b, am_b)) in enumerate(zip(base, alt)):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"pos {i}: logits differ"
+        assert am_a == am_b
+    assert np.array_equal(kb.view(np.uint32), ka.view(np.uint32))
+    assert np.array_equal(vb.view(np.uint32), va.view(np.uint32))
