@@ -237,8 +237,10 @@ __device__ __forceinline__ void mega_stage(Src src, int n, const float* __restri
 // MEGA_DSPLIT waves may own.
 #define MEGA_DSPLIT 4
 #define MEGA_DSPLIT_ROWS 16
-// Items in flight in the gate/up and split down-projection streams (Q4_0
-// weights; the Q8_0 buffers are twice as large and keep two).
+// Items in flight in the gate/up and split down-projection streams of the
+// int8-plane layers (Q4_0 and Q8_0; with Q8_0 the third item makes the
+// kernel spill ~92 bytes per lane, which slows its attention by ~1.5 us per
+// layer at 16k positions, less than the two streams gain).
 #ifndef MEGA_DEPTH_GU
 #define MEGA_DEPTH_GU 3
 #endif
@@ -1057,7 +1059,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
           }
         }
       };
-      constexpr int DG = IQ && LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_GU : 2;
+      constexpr int DG = IQ ? MEGA_DEPTH_GU : 2;
       mv_stream<LF, RG, UN, true, IQ, DG>(gu_units, unit, arrive, stage, epi, X.src(LL), lane, pre);
       MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 7);
     }
@@ -1177,7 +1179,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             __hip_atomic_store(gptr(reinterpret_cast<uint64_t*>(dq + row0 + (uint32_t)k * RD)), v2, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);  // the unit's two rows in one store
           };
-          constexpr int DD = LF == TALOS_FMT_Q4_0 ? MEGA_DEPTH_DQ : 2;
+          constexpr int DD = MEGA_DEPTH_DQ;
           mv_stream<LF, RD, UN, false, true, DD>((int)(rpw / RD), unit, arrive, stage, epi, X.src(LL), lane, pre);
         } else if (P.dsplit) {
           // The down rows in column quarters: the four waves of a team (waves
