@@ -190,6 +190,30 @@ int talos_hip_bench_copy(talos_hip_ctx* ctx, size_t nbytes, uint32_t reps, float
 int talos_hip_phase_timeline(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint64_t* marks, size_t cap,
                              uint32_t* nblocks, uint32_t* slots, double* tick_ns);
 
+/* Poll limit of the persistent kernel's bounded waits (grid barriers and
+ * producer waits; default 2^20 polls, 0 restores the default).  A wait that
+ * reaches it stops waiting, later barriers of the launch are skipped, every
+ * workgroup runs to the end and the step returns TALOS_ERR_HIP (the results
+ * of that step are invalid; the next step starts clean).  A tuning and test
+ * knob: a tiny limit forces that error path from the host.  No reference
+ * counterpart (the Metal backend has no cross-workgroup waits). */
+int talos_hip_set_spin_limit(talos_hip_ctx* ctx, uint32_t polls);
+
+/* Implementations of the token step (talos_hip_path). */
+enum {
+  TALOS_PATH_NONE = 0,
+  TALOS_PATH_PERSISTENT = 1,    /* one persistent-kernel launch per token */
+  TALOS_PATH_GRAPH = 2,         /* ~5 fused kernels per layer replayed as one hipGraph */
+  TALOS_PATH_GRAPH_GENERIC = 3  /* the graph with generic-shape kernels for some steps (any head_dim,
+                                   group, mixed formats) */
+};
+
+/* Which implementation runs this context's token step for the resident
+ * weights (every tensor the forward needs must be uploaded; the choice is
+ * made as at the first forward).  No reference counterpart: the Metal
+ * backend has one path (metal/mod.rs:368-520); this one picks per model. */
+int talos_hip_path(talos_hip_ctx* ctx, int* path);
+
 /* The context's HIP stream (hipStream_t), for callers that time or order
  * work around talos_hip_matvec_dev. */
 void* talos_hip_stream(talos_hip_ctx* ctx);

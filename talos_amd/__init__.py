@@ -25,6 +25,9 @@ STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_DTYPE", 4: "ERR_SHAPE",
           5: "ERR_MISSING_WEIGHT", 6: "ERR_POS", 7: "ERR_TOKEN"}
 
 
+PATHS = {0: "none", 1: "persistent", 2: "graph", 3: "graph_generic"}
+
+
 class TalosError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"{STATUS.get(code, code)}: {msg}")
@@ -76,6 +79,8 @@ _SIGS = {
     "talos_hip_bench_copy": (C.c_int, [_P, C.c_size_t, C.c_uint32, _F]),
     "talos_hip_phase_timeline": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64), C.c_size_t,
                                             _U32, _U32, C.POINTER(C.c_double)]),
+    "talos_hip_path": (C.c_int, [_P, C.POINTER(C.c_int)]),
+    "talos_hip_set_spin_limit": (C.c_int, [_P, C.c_uint32]),
     "talos_hip_stream": (_P, [_P]),
     "talos_hip_sync": (C.c_int, [_P]),
     # include/talos_host.h
@@ -239,6 +244,12 @@ class HipBackend:
         b = C.c_double()
         self._check(lib().talos_hip_bench_matvec(self._h, arr, len(names), reps, C.byref(us), C.byref(b)))
         return us.value, b.value
+
+    def path(self) -> str:
+        """The token step's implementation for the resident weights."""
+        p = C.c_int()
+        self._check(lib().talos_hip_path(self._h, C.byref(p)))
+        return PATHS[p.value]
 
     def stream(self) -> int:
         return lib().talos_hip_stream(self._h) or 0
@@ -493,6 +504,23 @@ class Model:
             raise TalosError(rc, lib().talos_hip_last_error(h).decode())
         t = marks[: nb.value * sl.value].reshape(nb.value, sl.value).astype(np.float64) * tick.value
         return t
+
+    def path(self) -> str:
+        """The token step's implementation: "persistent", "graph" or
+        "graph_generic" (talos_hip_path)."""
+        h = self.backend_handle()
+        p = C.c_int()
+        rc = lib().talos_hip_path(h, C.byref(p))
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
+        return PATHS[p.value]
+
+    def set_spin_limit(self, polls: int):
+        """Poll limit of the persistent kernel's bounded waits (0: default)."""
+        h = self.backend_handle()
+        rc = lib().talos_hip_set_spin_limit(h, polls)
+        if rc:
+            raise TalosError(rc, lib().talos_hip_last_error(h).decode())
 
     def backend_handle(self) -> int:
         h = lib().talos_model_backend(self._h)

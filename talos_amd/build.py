@@ -21,7 +21,8 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtalos_hip.so")
 
 ARCH = "gfx950"
-HIP_SOURCES = ["talos_hip.hip"]
+HIP_SOURCES = ["talos_hip.hip", "mega_inst_q4_mfma.hip", "mega_inst_q4_q6k.hip", "mega_inst_q4_q4.hip",
+               "mega_inst_q8_wide.hip", "mega_inst_q8_small.hip", "mega_inst_f32.hip"]
 HOST_SOURCES = ["host/gguf.cpp", "host/synth.cpp", "host/model.cpp", "host/host_capi.cpp"]
 
 HIPCC_FLAGS = [

@@ -50,6 +50,7 @@ __device__ __forceinline__ void st_coh4(float* p, f4 v) {
 // Wait until this thread's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Default poll limit of every bounded wait (MegaParams::spin_limit).
 #define TALOS_SPIN_LIMIT (1u << 20)
 
 struct GridSync {
@@ -57,6 +58,7 @@ struct GridSync {
   uint32_t* go;     // release word written by block 0
   uint32_t* err;    // set to 1 when a wait timed out
   uint32_t nblocks;
+  uint32_t spin;    // polls before a wait gives up
 };
 
 // Shared flag: a wait timed out before this barrier, so it is skipped.
@@ -89,7 +91,7 @@ __device__ __forceinline__ void grid_wait(const GridSync& g, uint32_t ep) {
       for (uint32_t w = threadIdx.x; w < g.nblocks; w += blockDim.x) {
         uint32_t s = 0;
         while ((int32_t)(ld_coh_u(g.flags + w * 16) - ep) < 0) {
-          if (++s > TALOS_SPIN_LIMIT) {
+          if (++s > g.spin) {
             st_coh_u(g.err, 1u);
             break;
           }
@@ -101,7 +103,7 @@ __device__ __forceinline__ void grid_wait(const GridSync& g, uint32_t ep) {
   } else if (threadIdx.x == 0 && !skip) {
     uint32_t s = 0;
     while ((int32_t)(ld_coh_u(g.go) - ep) < 0) {
-      if (++s > TALOS_SPIN_LIMIT) {
+      if (++s > g.spin) {
         st_coh_u(g.err, 1u);
         break;
       }

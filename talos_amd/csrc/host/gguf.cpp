@@ -38,7 +38,7 @@ struct Cursor {
   const uint8_t* b;
   size_t len, pos = 0;
   const uint8_t* take(size_t n) {
-    if (n > len - pos) throw Error("unexpected end of file (need " + std::to_string(n) + " bytes at " +
+    if (n > len - pos) throw Error("GGUF data ends early: wanted " + std::to_string(n) + " bytes at " +
                                    std::to_string(pos) + ")");
     const uint8_t* p = b + pos;
     pos += n;
@@ -66,7 +66,7 @@ struct Cursor {
   }
   std::string str() {
     const uint64_t n = u64();
-    if (n > len - pos) throw Error("unexpected end of file (need " + std::to_string(n) + " bytes at " +
+    if (n > len - pos) throw Error("GGUF data ends early: wanted " + std::to_string(n) + " bytes at " +
                                    std::to_string(pos) + ")");
     const uint8_t* p = take((size_t)n);
     return std::string(reinterpret_cast<const char*>(p), (size_t)n);
@@ -96,12 +96,12 @@ MetaValue read_value(Cursor& c, uint32_t tag) {
         if (count > (c.len - c.pos) / 4) c.take(c.len - c.pos + 1);
         for (uint64_t i = 0; i < count; ++i) v.arr_f32.push_back(c.f32());
       } else {
-        throw Error("unsupported array element type tag " + std::to_string(inner));
+        throw Error("GGUF array holds values of unknown type " + std::to_string(inner));
       }
       return v;
     }
     default:
-      throw Error("unsupported metadata value type tag " + std::to_string(tag));
+      throw Error("GGUF metadata value of unknown type " + std::to_string(tag));
   }
 }
 
@@ -246,9 +246,9 @@ GgufFile GgufFile::from_bytes(std::vector<uint8_t> b) {
 void GgufFile::parse() {  // reader.rs:193-246
   Cursor c{data_, size_};
   const uint8_t* magic = c.take(4);
-  if (memcmp(magic, "GGUF", 4) != 0) throw Error("not a GGUF file (bad magic)");
+  if (memcmp(magic, "GGUF", 4) != 0) throw Error("file does not start with the GGUF magic");
   const uint32_t version = c.u32();
-  if (version != 3) throw Error("unsupported GGUF version " + std::to_string(version) + " (expected 3)");
+  if (version != 3) throw Error("GGUF version " + std::to_string(version) + " is not read here (only version 3)");
   const uint64_t n_t = c.u64(), n_kv = c.u64();
   for (uint64_t i = 0; i < n_kv; ++i) {
     std::string key = c.str();
@@ -256,7 +256,7 @@ void GgufFile::parse() {  // reader.rs:193-246
     try {
       meta_[key] = read_value(c, tag);
     } catch (const Error& e) {
-      throw Error("reading metadata key \"" + key + "\": " + e.what());
+      throw Error("metadata entry \"" + key + "\": " + e.what());
     }
   }
   for (uint64_t i = 0; i < n_t; ++i) {
@@ -267,14 +267,14 @@ void GgufFile::parse() {  // reader.rs:193-246
     for (uint32_t d = 0; d < nd; ++d) t.dims.push_back(c.u64());
     const uint32_t tag = c.u32();
     if (!ggml_type_from_u32(tag, &t.dtype))
-      throw Error("tensor \"" + t.name + "\" has unsupported ggml type " + std::to_string(tag));
+      throw Error("tensor \"" + t.name + "\": ggml type tag not handled: " + std::to_string(tag));
     t.offset = c.u64();
     by_name_[t.name] = tensors_.size();
     tensors_.push_back(std::move(t));
   }
   data_start_ = (c.pos + kAlign - 1) / kAlign * kAlign;
   if (data_start_ > size_)
-    throw Error("data section start " + std::to_string(data_start_) + " past end of file " + std::to_string(size_));
+    throw Error("tensor data would start at byte " + std::to_string(data_start_) + " of a " + std::to_string(size_) + "-byte file");
 }
 
 const MetaValue* GgufFile::metadata(const std::string& key) const {
@@ -317,8 +317,8 @@ const TensorInfo* GgufFile::tensor_info(const std::string& name) const {
 
 const float* GgufFile::tensor_f32(const std::string& name, size_t* n) const {
   const TensorInfo* t = tensor_info(name);
-  if (!t) throw Error("no tensor named \"" + name + "\"");
-  if (t->dtype != GgmlType::F32) throw Error("tensor \"" + name + "\" is not F32");
+  if (!t) throw Error("model has no tensor \"" + name + "\"");
+  if (t->dtype != GgmlType::F32) throw Error("tensor \"" + name + "\" must be stored as F32");
   size_t len;
   GgmlType ty;
   const uint8_t* p = tensor_raw(name, &len, &ty);
@@ -328,10 +328,10 @@ const float* GgufFile::tensor_f32(const std::string& name, size_t* n) const {
 
 const uint8_t* GgufFile::tensor_raw(const std::string& name, size_t* len, GgmlType* type) const {
   const TensorInfo* t = tensor_info(name);
-  if (!t) throw Error("no tensor named \"" + name + "\"");
+  if (!t) throw Error("model has no tensor \"" + name + "\"");
   uint64_t elems = 1;
   for (uint64_t d : t->dims) {
-    if (d && elems > UINT64_MAX / d) throw Error("tensor byte length overflow");
+    if (d && elems > UINT64_MAX / d) throw Error("tensor size overflows 64 bits");
     elems *= d;
   }
   const size_t blk = block_elems(t->dtype);
@@ -341,7 +341,7 @@ const uint8_t* GgufFile::tensor_raw(const std::string& name, size_t* len, GgmlTy
   const uint64_t blen = elems / blk * block_bytes(t->dtype);
   const uint64_t start = (uint64_t)data_start_ + t->offset;
   if (start < t->offset || start + blen < start || start + blen > size_)
-    throw Error("tensor \"" + name + "\" data range past end of file");
+    throw Error("tensor \"" + name + "\" runs past the end of the file");
   *len = (size_t)blen;
   *type = t->dtype;
   return data_ + start;

@@ -14,15 +14,15 @@ void check(talos_hip_ctx* ctx, int rc) {
 Config Config::from_gguf(const GgufFile& g) {
   const std::string* arch = g.get_str("general.architecture");
   if (!arch || *arch != "llama")
-    throw Error("unsupported architecture \"" + (arch ? *arch : std::string()) + "\" (expected \"llama\")");
+    throw Error("general.architecture is \"" + (arch ? *arch : std::string()) + "\"; only \"llama\" models load");
   Config c;
   auto u = [&](const char* k) {
     uint32_t v;
-    if (!g.get_u32(k, &v)) throw Error(std::string("missing metadata key ") + k);
+    if (!g.get_u32(k, &v)) throw Error(std::string("model metadata lacks ") + k);
     return v;
   };
   const auto* toks = g.get_arr_str("tokenizer.ggml.tokens");
-  if (!toks) throw Error("missing tokenizer.ggml.tokens (needed for vocab size)");
+  if (!toks) throw Error("model metadata lacks tokenizer.ggml.tokens, which sets the vocabulary size");
   c.vocab_size = (uint32_t)toks->size();
   c.n_layer = u("llama.block_count");
   c.n_head = u("llama.attention.head_count");
@@ -70,12 +70,12 @@ Weights Weights::from_gguf(const GgufFile& g, const Config& cfg) {
     lw.ffn_up = QTensor::bind(g, p + "ffn_up.weight", ff, c);
     lw.ffn_down = QTensor::bind(g, p + "ffn_down.weight", c, ff);
     for (const QTensor* n : {&lw.attn_norm, &lw.ffn_norm})
-      if (n->dtype != GgmlType::F32) throw Error("tensor \"" + n->name + "\" is not F32");
+      if (n->dtype != GgmlType::F32) throw Error("norm \"" + n->name + "\" must be stored as F32");
     w.layers.push_back(std::move(lw));
   }
   w.token_embd = QTensor::bind(g, "token_embd.weight", v, c);
   w.output_norm = QTensor::bind(g, "output_norm.weight", 1, c);
-  if (w.output_norm.dtype != GgmlType::F32) throw Error("tensor \"output_norm.weight\" is not F32");
+  if (w.output_norm.dtype != GgmlType::F32) throw Error("norm \"output_norm.weight\" must be stored as F32");
   w.output = QTensor::bind(g, "output.weight", v, c);
   return w;
 }
@@ -91,8 +91,8 @@ std::unique_ptr<Model> Model::load(const std::string& path, int device) {
 std::unique_ptr<Model> Model::from_gguf(GgufFile g, int device) {
   Config cfg = Config::from_gguf(g);
   if (cfg.n_head_kv == 0 || cfg.n_head % cfg.n_head_kv != 0)
-    throw Error("head_count " + std::to_string(cfg.n_head) + " must be a positive multiple of head_count_kv " +
-                std::to_string(cfg.n_head_kv));
+    throw Error("attention head_count " + std::to_string(cfg.n_head) + " is not divisible by a nonzero head_count_kv (" +
+                std::to_string(cfg.n_head_kv) + ")");
   std::unique_ptr<Model> m(new Model(std::move(g), device));
   m->cfg = cfg;
   m->w_ = Weights::from_gguf(m->gguf_, m->cfg);

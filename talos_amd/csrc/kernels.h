@@ -466,6 +466,122 @@ __global__ __launch_bounds__(256) void k_attn(AttnParams P) {
   if (tid == 0) atomicExch(&P.count[j], 0u);
 }
 
+// ------------------------------------------------ generic-shape kernels --
+// The forms of a layer that any Llama config takes (src/model/llama.rs:
+// 45-51 accepts every n_head that n_head_kv divides): q/k/v or gate/up of
+// different formats, any head_dim (odd included), n_embd not a multiple of
+// n_head, GQA groups of any size.  They follow the reference's steps one by
+// one: raw projections, then RoPE and the cache append, then attention in
+// three passes over a scores buffer [n_head][context_length] (the passes of
+// src/math/metal/kernels.metal:186-237, which take the same shapes).
+
+// RoPE (src/math/ops.rs:48-61: adjacent pairs (2i, 2i+1), i < head_dim / 2,
+// of each head, theta from the host-built table; an odd head_dim leaves each
+// head's last element as it is) of the raw q into q_out, elements past the
+// heads (n_embd > n_head * head_dim) copied; the raw k rotated into the K
+// cache row at `pos` and the raw v copied into the V row (the append of
+// src/kv_cache.rs).  One thread per element; inputs and outputs are separate
+// buffers, so a pair is read whole by both of its threads.
+__device__ __forceinline__ float rope_elem(const float* __restrict__ src, uint32_t i, uint32_t hd, int pos,
+                                           const float* __restrict__ rope) {
+  const uint32_t half = hd / 2, h = i / hd, w = i % hd, p = w / 2;
+  if (p >= half) return src[i];
+  const float c = rope[((size_t)pos * half + p) * 2 + 0];
+  const float sn = rope[((size_t)pos * half + p) * 2 + 1];
+  const float a = src[h * hd + 2 * p], b = src[h * hd + 2 * p + 1];
+  return (w & 1) ? a * sn + b * c : a * c - b * sn;
+}
+
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_rope_qkv(const float* __restrict__ qraw, const float* __restrict__ kraw,
+                                                  const float* __restrict__ vraw, float* __restrict__ q_out,
+                                                  float* __restrict__ kc, float* __restrict__ vc,
+                                                  const float* __restrict__ rope, const int32_t* __restrict__ state,
+                                                  uint32_t n, uint32_t n_head, uint32_t hd, uint32_t kv_dim) {
+  const int pos = state[ST_POS];
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) q_out[i] = i < n_head * hd ? rope_elem(qraw, i, hd, pos, rope) : qraw[i];
+  if (i < kv_dim) {
+    kc[(size_t)pos * kv_dim + i] = rope_elem(kraw, i, hd, pos, rope);
+    vc[(size_t)pos * kv_dim + i] = vraw[i];
+  }
+}
+
+// h[i] = silu(g[i]) * u[i] (src/math/ops.rs:28-37), for gate and up rows of
+// different formats (computed by two matvecs).
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                                                float* __restrict__ h, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) h[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+// Attention in three passes, any head_dim and group (src/model/llama.rs:
+// 135-155).  Pass 1: scores[h][t] = <q_h, K_t of KV head h / group> * scale
+// for t <= pos; one thread per (head, position), q_h in LDS.
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kc,
+                                                     float* __restrict__ scores, const int32_t* __restrict__ state,
+                                                     uint32_t hd, uint32_t kv_dim, uint32_t group, uint32_t ctx,
+                                                     float scale) {
+  extern __shared__ float qs[];
+  const int seq = state[ST_POS] + 1;
+  const uint32_t h = blockIdx.x, kvh = h / group;
+  const int t0 = (int)blockIdx.y * 256;
+  if (t0 >= seq) return;  // uniform per block
+  for (uint32_t i = threadIdx.x; i < hd; i += 256) qs[i] = q[(size_t)h * hd + i];
+  __syncthreads();
+  const int t = t0 + (int)threadIdx.x;
+  if (t >= seq) return;
+  const float* kp = kc + (size_t)t * kv_dim + (size_t)kvh * hd;
+  float d = 0.f;
+  for (uint32_t i = 0; i < hd; ++i) d += qs[i] * kp[i];
+  scores[(size_t)h * ctx + t] = d * scale;
+}
+
+// Pass 2 (src/math/ops.rs:15-25): per head, scores become
+// exp(s - max) / sum over t <= pos.  One block per head; fixed-order
+// reductions.
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_attn_softmax(float* __restrict__ scores, const int32_t* __restrict__ state,
+                                                      uint32_t ctx) {
+  __shared__ float red[8];
+  const int seq = state[ST_POS] + 1;
+  float* s = scores + (size_t)blockIdx.x * ctx;
+  float m = -INFINITY;
+  for (int t = threadIdx.x; t < seq; t += 256) m = fmaxf(m, s[t]);
+  m = wave_max(m);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float l = 0.f;
+  for (int t = threadIdx.x; t < seq; t += 256) {
+    const float e = expf(s[t] - m);
+    s[t] = e;
+    l += e;
+  }
+  l = block_sum(l, red, 4);
+  const float inv = 1.0f / l;
+  for (int t = threadIdx.x; t < seq; t += 256) s[t] *= inv;
+}
+
+// Pass 3: out[h][d] = sum_t p[h][t] V_t[kvh][d].  Block (head, 64 dims): four
+// position subsets per dim, summed in subset order.
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_attn_out(const float* __restrict__ scores, const float* __restrict__ vc,
+                                                  float* __restrict__ out, const int32_t* __restrict__ state,
+                                                  uint32_t hd, uint32_t kv_dim, uint32_t group, uint32_t ctx) {
+  __shared__ float part[4][64];
+  const int seq = state[ST_POS] + 1;
+  const uint32_t h = blockIdx.x, kvh = h / group;
+  const uint32_t dl = threadIdx.x & 63, sub = threadIdx.x >> 6;
+  const uint32_t d = blockIdx.y * 64 + dl;
+  const float* s = scores + (size_t)h * ctx;
+  float acc = 0.f;
+  if (d < hd)
+    for (int t = (int)sub; t < seq; t += 4) acc = __builtin_fmaf(s[t], vc[(size_t)t * kv_dim + (size_t)kvh * hd + d], acc);
+  part[sub][dl] = acc;
+  __syncthreads();
+  if (sub == 0 && d < hd) out[(size_t)h * hd + d] = ((part[0][dl] + part[1][dl]) + part[2][dl]) + part[3][dl];
+}
+
 // --------------------------------------------------------------- k_embed --
 // x = dequant_row(token_embd, token) (src/model/weights.rs:58-62,
 // src/gguf/dtype.rs:64-121), on the device, from the repacked layout.
@@ -505,7 +621,7 @@ __device__ __forceinline__ float dq_elem(const DevMat& M, uint32_t r, uint32_t e
   }
 }
 
-__global__ __launch_bounds__(256) void k_embed(DevMat M, const int32_t* state, float* x) {
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_embed(DevMat M, const int32_t* state, float* x) {
   const uint32_t tok = (uint32_t)state[ST_TOKEN];
   for (uint32_t e = threadIdx.x; e < M.cols; e += 256) x[e] = dq_elem(M, tok, e);
 }
@@ -513,11 +629,11 @@ __global__ __launch_bounds__(256) void k_embed(DevMat M, const int32_t* state, f
 // ------------------------------------------------------- k_copy, k_fill --
 // Plain device copy (reference point for HBM bandwidth and for scaling the
 // FETCH_SIZE / WRITE_SIZE counters), and a fill of distinct values.
-__global__ __launch_bounds__(256) void k_copy(const u4* __restrict__ src, u4* __restrict__ dst, size_t n16) {
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_copy(const u4* __restrict__ src, u4* __restrict__ dst, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
     __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
-__global__ __launch_bounds__(256) void k_fill(u4* __restrict__ dst, size_t n16) {
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_fill(u4* __restrict__ dst, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) {
     const uint32_t v = (uint32_t)i * 2654435761u;
     dst[i] = u4{v, v + 1, v + 2, v + 3};
@@ -526,7 +642,7 @@ __global__ __launch_bounds__(256) void k_fill(u4* __restrict__ dst, size_t n16) 
 
 // --------------------------------------------------------------- k_norm --
 // hidden = rmsnorm(x, output_norm) (src/model/llama.rs:180-181).
-__global__ __launch_bounds__(256) void k_norm(const float* x, const float* w, float eps, uint32_t n, float* out) {
+static __global__ __attribute__((unused)) __launch_bounds__(256) void k_norm(const float* x, const float* w, float eps, uint32_t n, float* out) {
   __shared__ float red[8];
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < n; i += 256) ss += x[i] * x[i];
@@ -541,7 +657,7 @@ __global__ __launch_bounds__(256) void k_norm(const float* x, const float* w, fl
 // is set on the device: the argmax itself (2, the greedy loop, which also
 // appends it to `tokens`) or the next fed prompt token (3) -- both loops run
 // without host round trips.
-__global__ __launch_bounds__(1024) void k_argmax(const float* logits, uint32_t n, int32_t* state,
+static __global__ __attribute__((unused)) __launch_bounds__(1024) void k_argmax(const float* logits, uint32_t n, int32_t* state,
                                                  int32_t* tokens, int advance) {
   __shared__ int32_t sk[16];
   __shared__ int32_t si[16];

@@ -62,6 +62,7 @@ struct MegaParams {
   int argmax;  // 0: none, 1: argmax into state, 2: + greedy advance, 3: + feed advance (advance_state)
   int prefetch;  // issue each matvec phase's first weight loads before its barrier wait
   uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
+  uint32_t spin_limit; // polls before a bounded wait gives up (then ST_ERR is set)
 };
 
 // Read-only tables read through the constant address space compile to
@@ -702,6 +703,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   G.go = P.sync + nb * 16;
   G.err = reinterpret_cast<uint32_t*>(P.state + ST_ERR);
   G.nblocks = nb;
+  G.spin = P.spin_limit;
   uint32_t* epoch_p = P.sync + nb * 16 + 16;
   uint32_t* done = P.sync + nb * 16 + 32;
   int32_t* amx = reinterpret_cast<int32_t*>(P.sync + nb * 16 + 64);
@@ -898,7 +900,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
               const uint32_t b = (u % tw) / MEGA_NW;
               uint32_t k = 0;
               while ((int32_t)(ld_coh_u(G.flags + b * 16) - ep) < 0) {
-                if (++k > TALOS_SPIN_LIMIT) {
+                if (++k > G.spin) {
                   st_coh_u(G.err, 1u);
                   break;
                 }
@@ -971,7 +973,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             if (!barrier_skip() && threadIdx.x < o_prod) {
               uint32_t k = 0;
               while ((int32_t)(ld_coh_u(G.flags + threadIdx.x * 16) - ep) < 0) {
-                if (++k > TALOS_SPIN_LIMIT) {
+                if (++k > G.spin) {
                   st_coh_u(G.err, 1u);
                   break;
                 }
@@ -1157,7 +1159,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
                   for (uint32_t b = b0 + threadIdx.x; b <= b1 && b < nb; b += MEGA_NT) {
                     uint32_t k = 0;
                     while ((int32_t)(ld_coh_u(G.flags + b * 16) - ep) < 0) {
-                      if (++k > TALOS_SPIN_LIMIT) {
+                      if (++k > G.spin) {
                         st_coh_u(G.err, 1u);
                         break;
                       }

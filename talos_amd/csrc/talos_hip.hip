@@ -26,6 +26,7 @@
 
 #include "../../include/talos_hip.h"
 #include "mega.h"
+#include "mega_inst.h"
 
 namespace {
 
@@ -69,6 +70,14 @@ struct talos_hip_ctx {
   uint32_t* count = nullptr;
   int32_t* tokens = nullptr;
   float* rope = nullptr;
+  // generic-shape graph path: raw projections and the attention scores
+  float* qraw = nullptr;   // [n_embd]
+  float* kraw = nullptr;   // [kv_dim]
+  float* vraw = nullptr;   // [kv_dim]
+  float* graw = nullptr;   // [n_ff]
+  float* uraw = nullptr;   // [n_ff]
+  float* scores = nullptr; // [n_head][context_length]
+  int path = TALOS_PATH_NONE;  // decided with the persistent-kernel set-up
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -120,6 +129,7 @@ struct talos_hip_ctx {
   // TALOS_HIP_ATTN_WAIT=0 keeps a grid barrier in front of the attention.
   bool allow_attn_wait = true;
   int mega_mode = 0;  // MEGA_MM_* of the chosen instantiation
+  uint32_t spin_limit = TALOS_SPIN_LIMIT;  // talos_hip_set_spin_limit
   MegaParams mp{};
 };
 
@@ -269,6 +279,17 @@ int layout_need(uint32_t fmt) { return 1 << fmt_xlayout(fmt); }
     }                                                                         \
   } while (0)
 
+// Let kernel k take up to `bytes` of LDS in all (dynamic plus its own static
+// arrays).  A refused request leaves the kernel at the default limit, and
+// the runtime's last-error state is cleared so that it does not surface in
+// a later hipGetLastError.
+void set_max_lds(const void* k, int bytes) {
+  hipFuncAttributes a{};
+  int dyn = bytes;
+  if (hipFuncGetAttributes(&a, k) == hipSuccess) dyn -= (int)a.sharedSizeBytes;
+  if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, dyn) != hipSuccess) (void)hipGetLastError();
+}
+
 template <uint32_t F>
 void set_lds_attr_fmt(int bytes) {
   for (const void* k : {(const void*)k_qkv<F, mv_rows(F), 1>, (const void*)k_qkv<F, mv_rows(F), 2>,
@@ -276,7 +297,7 @@ void set_lds_attr_fmt(int bytes) {
                         (const void*)k_rows<F, mv_rows(F), 2>, (const void*)k_rows<F, mv_rows(F), 4>,
                         (const void*)k_gateup<F, mv_rows(F), 1>, (const void*)k_gateup<F, mv_rows(F), 2>,
                         (const void*)k_gateup<F, mv_rows(F), 4>})
-    (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    set_max_lds(k, bytes);
 }
 
 void plan(uint32_t units, uint32_t& upw, uint32_t& blocks) {
@@ -305,6 +326,14 @@ int alloc_acts(talos_hip_ctx* c) {
   c->x = reinterpret_cast<float*>(c->io + 16);
   HIPCHK(c, hipMalloc(&c->q, (size_t)cf.n_embd * 4));
   HIPCHK(c, hipMalloc(&c->atty, (size_t)cf.n_embd * 4));
+  // past the heads (n_embd > n_head * head_dim) the attention output stays 0
+  HIPCHK(c, hipMemsetAsync(c->atty, 0, (size_t)cf.n_embd * 4, c->stream));
+  HIPCHK(c, hipMalloc(&c->qraw, (size_t)cf.n_embd * 4));
+  HIPCHK(c, hipMalloc(&c->kraw, (size_t)c->kv_dim * 4));
+  HIPCHK(c, hipMalloc(&c->vraw, (size_t)c->kv_dim * 4));
+  HIPCHK(c, hipMalloc(&c->graw, (size_t)cf.n_ff * 4));
+  HIPCHK(c, hipMalloc(&c->uraw, (size_t)cf.n_ff * 4));
+  HIPCHK(c, hipMalloc(&c->scores, (size_t)cf.n_head * cf.context_length * 4));
   HIPCHK(c, hipMalloc(&c->h, (size_t)cf.n_ff * 4));
   HIPCHK(c, hipMalloc(&c->logits, (size_t)cf.vocab_size * 4));
   HIPCHK(c, hipMalloc(&c->hidden, (size_t)cf.n_embd * 4));
@@ -344,9 +373,6 @@ int layer_weights(talos_hip_ctx* c, uint32_t l, LayerW* w) {
       (rc = need_matrix(c, NM("ffn_down.weight"), n, cf.n_ff, &w->d)))
     return rc;
 #undef NM
-  if (w->k->type != w->q->type || w->v->type != w->q->type)
-    return fail(c, TALOS_ERR_DTYPE, "layer %u: attn_q/k/v must share one ggml type", l);
-  if (w->u->type != w->g->type) return fail(c, TALOS_ERR_DTYPE, "layer %u: ffn_gate/up must share one ggml type", l);
   return TALOS_OK;
 }
 
@@ -376,6 +402,70 @@ void enq_qkv(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
   plan(P.units[0] + P.units[1] + P.units[2], P.upw, blocks);
   TALOS_MV_LAUNCH(k_qkv, w.q->mat.fmt, mv_u(w.q->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, P.need),
                   c->stream, P);
+}
+
+// The layer forms the graph path can fuse: q/k/v in one kernel with RoPE in
+// its epilogue (one format, whole heads, even head_dim, rows in whole
+// units), gate/up in one kernel (one format); attention in one kernel per
+// KV-head slice (head_dim a multiple of 16 in [32, 128], group <= 8).
+bool fused_qkv(const talos_hip_ctx* c, const LayerW& w) {
+  const uint32_t R = (uint32_t)mv_rows(w.q->mat.fmt), n = c->cfg.n_embd;
+  return w.k->type == w.q->type && w.v->type == w.q->type && c->hd % 2 == 0 && n == c->cfg.n_head * c->hd &&
+         n % R == 0 && c->kv_dim % R == 0;
+}
+bool fused_gateup(const LayerW& w) { return w.u->type == w.g->type; }
+bool fast_attn(const talos_hip_ctx* c) {
+  return c->hd % 16 == 0 && c->hd >= 32 && c->hd <= 128 && c->group <= TALOS_MAX_GROUP &&
+         attn_lds_bytes(c->hd, c->group, c->nsplit, c->max_chunk) <= c->max_lds;
+}
+
+// out[rows] = W rmsnorm(x) (norm_w non-null) or W x, no residual.
+void enq_rows(talos_hip_ctx* c, const DevWeight* w, const float* x, uint32_t n, const float* norm_w, float* out) {
+  RowParams R{};
+  R.m = w->mat;
+  R.x = x;
+  R.n = n;
+  R.norm_w = norm_w;
+  R.eps = c->cfg.rms_eps;
+  R.out = out;
+  R.accumulate = 0;
+  R.units = (uint32_t)((w->rows + mv_rows(w->mat.fmt) - 1) / mv_rows(w->mat.fmt));
+  R.need = layout_need(w->mat.fmt);
+  uint32_t blocks;
+  plan(R.units, R.upw, blocks);
+  TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
+                  c->stream, R);
+}
+
+// q/k/v of different formats or shapes the fused epilogue does not take:
+// three raw projections, then RoPE and the cache append.
+void enq_qkv_split(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
+  const uint32_t n = c->cfg.n_embd;
+  enq_rows(c, w.q, c->x, n, w.an, c->qraw);
+  enq_rows(c, w.k, c->x, n, w.an, c->kraw);
+  enq_rows(c, w.v, c->x, n, w.an, c->vraw);
+  const uint32_t m = std::max(n, c->kv_dim);
+  hipLaunchKernelGGL(k_rope_qkv, dim3((m + 255) / 256), dim3(256), 0, c->stream, c->qraw, c->kraw, c->vraw, c->q,
+                     c->kc[l], c->vc[l], c->rope, (const int32_t*)c->io, n, c->cfg.n_head, c->hd, c->kv_dim);
+}
+
+void enq_gateup_split(talos_hip_ctx* c, const LayerW& w) {
+  const uint32_t n = c->cfg.n_embd, ff = c->cfg.n_ff;
+  enq_rows(c, w.g, c->x, n, w.fn, c->graw);
+  enq_rows(c, w.u, c->x, n, w.fn, c->uraw);
+  hipLaunchKernelGGL(k_swiglu, dim3((ff + 255) / 256), dim3(256), 0, c->stream, c->graw, c->uraw, c->h, ff);
+}
+
+// Attention of any head_dim and group: scores, softmax, weighted V rows.
+void enq_attn_generic(talos_hip_ctx* c, uint32_t l) {
+  const auto& cf = c->cfg;
+  const int32_t* st = (const int32_t*)c->io;
+  hipLaunchKernelGGL(k_attn_scores, dim3(cf.n_head, (cf.context_length + 255) / 256), dim3(256), c->hd * 4, c->stream,
+                     c->q, c->kc[l], c->scores, st, c->hd, c->kv_dim, c->group, cf.context_length,
+                     1.0f / sqrtf((float)c->hd));
+  hipLaunchKernelGGL(k_attn_softmax, dim3(cf.n_head), dim3(256), 0, c->stream, c->scores, st, cf.context_length);
+  hipLaunchKernelGGL(k_attn_out, dim3(cf.n_head, (c->hd + 63) / 64), dim3(256), 0, c->stream, c->scores, c->vc[l],
+                     c->atty, st, c->hd, c->kv_dim, c->group, cf.context_length);
 }
 
 void enq_attn(talos_hip_ctx* c, uint32_t l) {
@@ -469,10 +559,13 @@ int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
   for (uint32_t l = 0; l < cf.n_layer; ++l) {
     LayerW w;
     if ((rc = layer_weights(c, l, &w))) return rc;
-    enq_qkv(c, l, w);
-    enq_attn(c, l);
+    if (fused_qkv(c, w)) enq_qkv(c, l, w);
+    else enq_qkv_split(c, l, w);
+    if (fast_attn(c)) enq_attn(c, l);
+    else enq_attn_generic(c, l);
     enq_resid(c, w.o, c->atty, n, c->x);
-    enq_gateup(c, w);
+    if (fused_gateup(w)) enq_gateup(c, w);
+    else enq_gateup_split(c, w);
     enq_resid(c, w.d, c->h, cf.n_ff, c->x);
   }
   const float* onorm;
@@ -492,10 +585,33 @@ int enqueue_token(talos_hip_ctx* c, GraphKind kind) {
 
 int mega_setup(talos_hip_ctx* c);
 
-int get_graph(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t* out) {
+// The graph path's form for the resident weights: every layer fused and the
+// one-kernel attention, or some generic-shape kernels.
+int graph_path_kind(talos_hip_ctx* c, int* kind) {
+  *kind = fast_attn(c) ? TALOS_PATH_GRAPH : TALOS_PATH_GRAPH_GENERIC;
+  for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
+    LayerW w;
+    int rc = layer_weights(c, l, &w);
+    if (rc) return rc;
+    if (!fused_qkv(c, w) || !fused_gateup(w)) *kind = TALOS_PATH_GRAPH_GENERIC;
+  }
+  return TALOS_OK;
+}
+
+// Buffers and the persistent-kernel set-up for the resident weights; fixes
+// which path the token step takes.
+int prepare(talos_hip_ctx* c) {
   int rc;
   if ((rc = alloc_acts(c))) return rc;
   if ((rc = mega_setup(c))) return rc;
+  if (c->mega_fn) c->path = TALOS_PATH_PERSISTENT;
+  else if ((rc = graph_path_kind(c, &c->path))) return rc;
+  return TALOS_OK;
+}
+
+int get_graph(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t* out) {
+  int rc;
+  if ((rc = prepare(c))) return rc;
   if (c->mega_fn) {
     *out = nullptr;
     return TALOS_OK;
@@ -536,31 +652,15 @@ int check_device_err(talos_hip_ctx* c) {
 
 // ---- persistent path
 
-template <uint32_t LF, uint32_t OF, int UN, int UF, int UO, int DPL, int MM>
-const void* mega_pick(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, int mm) {
-  return (lf == LF && of == OF && un == UN && uf == UF && uo == UO && dpl == DPL && mm == MM)
-             ? (const void*)k_mega<LF, OF, UN, UF, UO, DPL, MM>
-             : nullptr;
-}
-
-// The instantiations this library carries: the 7B-shape Q4_0 model on the
-// matrix cores (n = 4096, ff = 14336 -> 4 and 14 tiles per wave), and the
-// vector-ALU streaming path with int8-plane x (Q4_0 / Q8_0) or f32 x for the
-// tested shapes of each format.
+// The instantiations this library carries (mega_inst_*.hip): the 7B-shape
+// Q4_0 model on the matrix cores (n = 4096, ff = 14336 -> 4 and 14 tiles per
+// wave), and the vector-ALU streaming path with int8-plane x (Q4_0 / Q8_0)
+// or f32 x for the tested shapes of each format.
 const void* mega_kernel_for(uint32_t lf, uint32_t of, int un, int uf, int uo, int dpl, int mm) {
-  constexpr int F = MEGA_MM_F32, M = MEGA_MM_MFMA, D = MEGA_MM_DOT4;
-  const void* f = nullptr;
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 4, 14, 1, 8, M>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 4, 1, 8, D>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q6_K, 2, 2, 1, 8, F>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 4, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q4_0, TALOS_FMT_Q4_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, D>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 2, 2, 2, 8, F>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, D>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_Q8_0, TALOS_FMT_Q8_0, 1, 1, 1, 4, F>(lf, of, un, uf, uo, dpl, mm);
-  if (!f) f = mega_pick<TALOS_FMT_F32, TALOS_FMT_F32, 2, 2, 2, 3, F>(lf, of, un, uf, uo, dpl, mm);
-  return f;
+  static const MegaInstFn fns[] = MEGA_INST_FNS;
+  for (MegaInstFn f : fns)
+    if (const void* k = f(lf, of, un, uf, uo, dpl, mm)) return k;
+  return nullptr;
 }
 
 // Prepare the persistent kernel for the resident weights; returns OK with
@@ -640,7 +740,7 @@ int mega_setup(talos_hip_ctx* c) {
   // MEGA_STAGE_MAX floats, head_dim a multiple of 16, at most MEGA_ATTN_HG
   // q heads per KV head.
   if (cf.n_embd % 16 || cf.n_ff % 16 || std::max(cf.n_embd, cf.n_ff) > MEGA_STAGE_MAX || c->hd % 16 ||
-      c->group > MEGA_ATTN_HG) {
+      c->group > MEGA_ATTN_HG || cf.n_embd != cf.n_head * c->hd) {
     c->mega_ready = true;
     return TALOS_OK;
   }
@@ -732,6 +832,7 @@ int mega_setup(talos_hip_ctx* c) {
 int mega_launch(talos_hip_ctx* c, GraphKind kind, uint64_t* timeline = nullptr) {
   MegaParams P = c->mp;
   P.timeline = timeline;
+  P.spin_limit = c->spin_limit;
   P.embed = device_token(kind);
   P.hidden_only = kind == G_HIDDEN;
   P.argmax = device_token(kind) ? (kind == G_TOKEN ? 1 : advance_mode(kind)) : 0;
@@ -783,14 +884,10 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   if (f.n_head % f.n_head_kv != 0)
     return fail(nullptr, TALOS_ERR_ARG, "head_count %u must be a positive multiple of head_count_kv %u", f.n_head,
                 f.n_head_kv);
-  if (f.n_embd % f.n_head != 0) return fail(nullptr, TALOS_ERR_ARG, "n_embd %u not divisible by n_head", f.n_embd);
+  // head_dim = n_embd / n_head, rounded down (src/model/config.rs); any
+  // value of at least 1 is served (the generic-shape kernels take odd ones)
   const uint32_t hd = f.n_embd / f.n_head;
-  if (hd % 16 != 0 || hd < 32 || hd > 128)
-    return fail(nullptr, TALOS_ERR_ARG, "head_dim %u unsupported (needs a multiple of 16 in [32, 128])", hd);
-  if (f.n_head / f.n_head_kv > TALOS_MAX_GROUP)
-    return fail(nullptr, TALOS_ERR_ARG, "GQA group %u exceeds %d", f.n_head / f.n_head_kv, TALOS_MAX_GROUP);
-  if (f.n_embd % 4 != 0 || f.n_ff % 4 != 0)
-    return fail(nullptr, TALOS_ERR_ARG, "n_embd and n_ff must be multiples of 4");
+  if (hd == 0) return fail(nullptr, TALOS_ERR_ARG, "n_embd %u < n_head %u leaves no head dimension", f.n_embd, f.n_head);
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0)
     return fail(nullptr, TALOS_ERR_HIP, "no HIP device available");
@@ -824,7 +921,10 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   // 512 * chunk positions the slices grow to ceil(ctx / 512).
   uint32_t ns = (f.context_length + TALOS_ATTN_CHUNK - 1) / TALOS_ATTN_CHUNK;
   c->nsplit = ns < 1 ? 1 : (ns > 512 ? 512 : ns);
-  c->max_chunk = (f.context_length + c->nsplit - 1) / c->nsplit;
+  // Longest live slice: up to TALOS_ATTN_CHUNK positions while the slice
+  // count follows the sequence, ceil(ctx / nsplit) once it is capped (a
+  // context that is not a multiple of the chunk still has chunk-long slices).
+  c->max_chunk = std::max<uint32_t>(TALOS_ATTN_CHUNK, (f.context_length + c->nsplit - 1) / c->nsplit);
   hipError_t e = hipSetDevice(f.device);
   if (e != hipSuccess) return fail(nullptr, TALOS_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
   hipDeviceProp_t prop;
@@ -838,6 +938,12 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   set_lds_attr_fmt<TALOS_FMT_Q4_0>((int)c->max_lds);
   set_lds_attr_fmt<TALOS_FMT_Q8_0>((int)c->max_lds);
   set_lds_attr_fmt<TALOS_FMT_Q6_K>((int)c->max_lds);
+  for (const void* k : {(const void*)k_attn_scores, (const void*)k_attn<2>, (const void*)k_attn<3>, (const void*)k_attn<4>,
+                        (const void*)k_attn<5>, (const void*)k_attn<6>, (const void*)k_attn<7>, (const void*)k_attn<8>})
+    set_max_lds(k, (int)c->max_lds);
+  if ((size_t)hd * 4 > c->max_lds)
+    return fail(nullptr, TALOS_ERR_ARG, "head_dim %u needs %zu B of LDS, device has %zu", hd, (size_t)hd * 4,
+                c->max_lds);
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
     return fail(nullptr, TALOS_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
 
@@ -870,7 +976,8 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
-                 c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart};
+                 c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart, c->qraw, c->kraw,
+                 c->vraw, c->graw, c->uraw, c->scores};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   if (c->h_io) (void)hipHostFree(c->h_io);
@@ -1357,6 +1464,23 @@ int talos_hip_phase_timeline(talos_hip_ctx* c, uint32_t token, uint32_t pos, uin
   (void)hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, c->cfg.device);
   *tick_ns = rate_khz > 0 ? 1e6 / rate_khz : 10.0;
   return rc;
+}
+
+int talos_hip_set_spin_limit(talos_hip_ctx* c, uint32_t polls) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  c->spin_limit = polls ? polls : TALOS_SPIN_LIMIT;
+  return TALOS_OK;
+}
+
+int talos_hip_path(talos_hip_ctx* c, int* path) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!path) return fail(c, TALOS_ERR_ARG, "null path");
+  if ((rc = set_device(c))) return rc;
+  if ((rc = prepare(c))) return rc;
+  *path = c->path;
+  return TALOS_OK;
 }
 
 void* talos_hip_stream(talos_hip_ctx* c) { return c ? (void*)c->stream : nullptr; }

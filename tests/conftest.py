@@ -26,3 +26,16 @@ def talos():
     import talos_amd
     talos_amd.lib()  # fails loudly if the library was not built
     return talos_amd
+
+
+def record_parity(case: str, worst: float, tol: float, **extra) -> None:
+    """Append one parity margin (worst max-abs difference against the
+    oracle, and the bar it was held to) to the JSON-lines file named by
+    TALOS_PARITY_LOG, when that is set."""
+    import json
+    path = os.environ.get("TALOS_PARITY_LOG")
+    if not path:
+        return
+    rec = {"case": case, "worst_max_abs": float(worst), "tol": float(tol), **extra}
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")

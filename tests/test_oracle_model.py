@@ -120,14 +120,18 @@ def np_forward(W, tokens, *, embd, n_head, n_head_kv, n_layer, theta=10000.0, ep
         return x / math.sqrt(np.mean(x * x) + eps) * w
 
     def rope(v, pos, nh):
-        v = v.reshape(nh, hd).copy()
+        # adjacent pairs (2i, 2i+1), i < hd // 2, of the first nh heads; an
+        # odd hd leaves each head's last element, and elements past the
+        # heads stay as they are
+        v = v.copy()
         i = np.arange(hd // 2)
         ang = pos * theta ** (-2.0 * i / hd)
         c, s = np.cos(ang), np.sin(ang)
-        x0, x1 = v[:, 0::2].copy(), v[:, 1::2].copy()
-        v[:, 0::2] = x0 * c - x1 * s
-        v[:, 1::2] = x0 * s + x1 * c
-        return v.reshape(-1)
+        for h in range(nh):
+            x0, x1 = v[h * hd + 2 * i].copy(), v[h * hd + 2 * i + 1].copy()
+            v[h * hd + 2 * i] = x0 * c - x1 * s
+            v[h * hd + 2 * i + 1] = x0 * s + x1 * c
+        return v
 
     K = [[] for _ in range(n_layer)]
     V = [[] for _ in range(n_layer)]
@@ -171,6 +175,33 @@ def test_forward_matches_float64_restatement(qtype, tol):
         got = m.forward(t, pos)
         d = float(np.abs(got - ref[pos]).max())
         assert d <= tol * max(1.0, float(np.abs(ref[pos]).max())), f"pos {pos}: {d}"
+    m.close()
+
+
+# Shapes the reference accepts beyond the benchmark ones (src/model/
+# llama.rs:45-51 asks only that n_head_kv divide n_head): its own GPU
+# contract model (tests/forward_gpu.rs:62: head_dim 4), an odd head_dim with
+# n_embd not a multiple of n_head (30 = 4 * 7 + 2), and a GQA group of 12.
+GENERIC_SHAPES = [
+    dict(embd=16, n_head=4, n_head_kv=2, ff=32, vocab=16, n_layer=2),
+    dict(embd=30, n_head=4, n_head_kv=2, ff=40, vocab=24, n_layer=2),
+    dict(embd=96, n_head=12, n_head_kv=1, ff=64, vocab=20, n_layer=2),
+]
+
+
+@pytest.mark.parametrize("shape", GENERIC_SHAPES, ids=["contract_hd4", "odd_hd7", "group12"])
+def test_forward_matches_float64_generic_shapes(shape):
+    rng = np.random.default_rng(29)
+    W = rand_model(rng, **shape, scale=0.5)
+    data = gguf_of(W, **shape)
+    m = O.OracleModel(data)
+    toks = [1, 3, 5, 7, 2, 4]
+    ref = np_forward(W, [t % shape["vocab"] for t in toks], embd=shape["embd"], n_head=shape["n_head"],
+                     n_head_kv=shape["n_head_kv"], n_layer=shape["n_layer"])
+    for pos, t in enumerate(toks):
+        got = m.forward(t % shape["vocab"], pos)
+        d = float(np.abs(got - ref[pos]).max())
+        assert d <= 1e-4 * max(1.0, float(np.abs(ref[pos]).max())), f"pos {pos}: {d}"
     m.close()
 
 
