@@ -123,6 +123,42 @@ int talos_hip_decode_greedy(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, ui
 int talos_hip_prefill(talos_hip_ctx* ctx, const uint32_t* tokens, uint32_t n, uint32_t pos, float* logits,
                       uint32_t* argmax);
 
+/* Draw one token from the logits of the context's latest forward step
+ * (src/sample.rs:19-76): temperature <= 0 is the greedy argmax (ties to the
+ * last index); otherwise the logits sorted descending by total_cmp (equal
+ * logits by descending index -- the reference's unstable sort leaves their
+ * order open), cut to the top_k largest (0: no cut, the reference's None),
+ * softmax at `temperature` over the kept set, cut to the shortest prefix
+ * whose cumulative probability reaches top_p (a value above 1, or NaN: no
+ * cut), and the first token whose cumulative probability reaches u times
+ * the kept mass.  u in [0, 1) is the caller's uniform draw, the reference's
+ * rng.gen::<f32>() (its StdRng stream is not reproduced here).  The draw
+ * runs on the device; only the token is read back. */
+int talos_hip_sample(talos_hip_ctx* ctx, float temperature, uint32_t top_k, float top_p, float u, uint32_t* token);
+
+/* The same draw from n device logits into a device uint32, enqueued on the
+ * context's stream and not waited for (the sampler's workspace is allocated
+ * by the library on first use and grown with n).  No reference
+ * counterpart: sampling inside a device-resident serving loop. */
+int talos_hip_sample_dev(talos_hip_ctx* ctx, const float* d_logits, uint32_t n, float temperature, uint32_t top_k,
+                         float top_p, float u, uint32_t* d_token);
+
+/* Sampled decode entirely on the device: starting from `token` at `pos`,
+ * run n_steps forwards, each followed by a draw (as talos_hip_sample, with
+ * draw u[s] for step s) that becomes the next input; writes the n_steps
+ * drawn tokens.  The loop of src/main.rs:100-112 with temperature > 0 and
+ * no EOS stop.  pos + n_steps <= context_length. */
+int talos_hip_decode_sample(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint32_t n_steps, float temperature,
+                            uint32_t top_k, float top_p, const float* u, uint32_t* tokens_out);
+
+/* Teacher-forced perplexity of tokens[0..n) (src/eval.rs:35-52): chunks of
+ * context_length tokens, each from position 0; within a chunk every
+ * position's forward scores the next token's -log softmax (src/eval.rs:
+ * 17-22, on the device, exponential sum in f64); ppl = exp(mean NLL).  The
+ * per-position NLLs go to nll (nullable; one per scored position, at most
+ * n - 1).  Replaces eval::perplexity's CPU Model::forward (eval.rs:46). */
+int talos_hip_perplexity(talos_hip_ctx* ctx, const uint32_t* tokens, uint32_t n, float* ppl, float* nll);
+
 /* Reset the cache for a new sequence.  Rows are position-indexed, so this
  * only records that no position is valid (the reference's GpuKv needs no
  * clear either, metal/mod.rs:443-454). */

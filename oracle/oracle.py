@@ -58,6 +58,8 @@ def lib() -> C.CDLL:
             "tor_swiglu": (None, [_F, _F, _F, C.c_size_t]),
             "tor_rope": (None, [_F, C.c_size_t, C.c_size_t, C.c_size_t, C.c_float]),
             "tor_argmax": (C.c_uint32, [_F, C.c_size_t]),
+            "tor_sample": (C.c_uint32, [_F, C.c_size_t, C.c_float, C.c_size_t, C.c_int, C.c_float, C.c_float]),
+            "tor_token_nll": (C.c_float, [_F, C.c_size_t, C.c_uint32]),
             "tor_model_load": (C.c_void_p, [C.c_void_p, C.c_size_t, C.c_int, C.c_char_p, C.c_size_t]),
             "tor_model_free": (None, [C.c_void_p]),
             "tor_model_config": (None, [C.c_void_p, C.POINTER(Config)]),
@@ -180,6 +182,39 @@ def rope(v, pos, n_head, head_dim, freq_base) -> np.ndarray:
 def argmax(logits) -> int:
     logits = np.ascontiguousarray(logits, np.float32)
     return lib().tor_argmax(_f(logits), logits.size)
+
+
+def sample(logits, temperature: float, top_k=None, top_p=None, u: float = 0.5) -> int:
+    """src/sample.rs:19-76 with the rng draw passed in as u in [0, 1)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().tor_sample(_f(logits), logits.size, temperature, 0 if top_k is None else int(top_k),
+                            0 if top_p is None else 1, 0.0 if top_p is None else float(top_p), u)
+
+
+def token_nll(logits, target: int) -> float:
+    """src/eval.rs:17-22."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    return lib().tor_token_nll(_f(logits), logits.size, target)
+
+
+def perplexity(model, tokens) -> tuple:
+    """src/eval.rs:35-52 on an OracleModel: chunks of context_length, each
+    from a reset cache, the NLL of every next token summed in f64.
+    Returns (perplexity, per-position NLLs)."""
+    assert len(tokens) >= 2
+    ctx = model.cfg.context_length
+    nll, nlls = 0.0, []
+    for c0 in range(0, len(tokens), ctx):
+        chunk = tokens[c0:c0 + ctx]
+        if len(chunk) < 2:
+            break
+        model.reset()
+        for pos in range(len(chunk) - 1):
+            lg = model.forward(chunk[pos], pos)
+            v = token_nll(lg, chunk[pos + 1])
+            nlls.append(v)
+            nll += float(v)
+    return float(np.float32(np.exp(nll / len(nlls)))), nlls
 
 
 class OracleModel:

@@ -389,6 +389,85 @@ uint32_t tor_argmax(const float *logits, size_t n) {
   return best;
 }
 
+/* ------------------------------------------------ sample.rs:19-76 -- */
+
+typedef struct {
+  int32_t key;
+  uint32_t idx;
+} tor_rank;
+
+/* descending total_cmp; equal logits in descending index order (the
+ * reference's sort_unstable_by leaves the order of equal logits open; this
+ * order makes top-1 the argmax, whose ties go to the last index). */
+static int cmp_desc(const void *a, const void *b) {
+  const tor_rank *x = (const tor_rank *)a, *y = (const tor_rank *)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1;
+  return x->idx > y->idx ? -1 : (x->idx < y->idx ? 1 : 0);
+}
+
+/* sample(logits, temperature, top_k, top_p, rng) with the draw
+ * rng.gen::<f32>() passed in as `u` (in [0, 1)); top_k == 0 is None,
+ * has_top_p == 0 is None.  Every step in f32, sums sequential, as the
+ * reference. */
+uint32_t tor_sample(const float *logits, size_t n, float temperature, size_t top_k, int has_top_p, float top_p,
+                    float u) {
+  if (temperature <= 0.0f) return tor_argmax(logits, n);
+  tor_rank *idx = (tor_rank *)malloc(n * sizeof(tor_rank));
+  float *probs = (float *)malloc(n * sizeof(float));
+  for (size_t i = 0; i < n; ++i) {
+    idx[i].key = total_key(logits[i]);
+    idx[i].idx = (uint32_t)i;
+  }
+  qsort(idx, n, sizeof(tor_rank), cmp_desc);
+  size_t keep = top_k == 0 ? n : (top_k < 1 ? 1 : (top_k > n ? n : top_k));
+  const float maxv = logits[idx[0].idx];
+  float sum = 0.0f;
+  for (size_t j = 0; j < keep; ++j) {
+    probs[j] = expf((logits[idx[j].idx] - maxv) / temperature);
+  }
+  for (size_t j = 0; j < keep; ++j) sum += probs[j];
+  for (size_t j = 0; j < keep; ++j) probs[j] /= sum;
+  size_t cutoff = keep;
+  if (has_top_p) {
+    float c = 0.0f;
+    for (size_t j = 0; j < keep; ++j) {
+      c += probs[j];
+      if (c >= top_p) {
+        cutoff = j + 1;
+        break;
+      }
+    }
+  }
+  float total = 0.0f;
+  for (size_t j = 0; j < cutoff; ++j) total += probs[j];
+  const float r = u * total;
+  float acc = 0.0f;
+  uint32_t out = idx[cutoff - 1].idx;
+  for (size_t j = 0; j < cutoff; ++j) {
+    acc += probs[j];
+    if (acc >= r) {
+      out = idx[j].idx;
+      break;
+    }
+  }
+  free(idx);
+  free(probs);
+  return out;
+}
+
+/* ---------------------------------------------------- eval.rs:17-22 -- */
+
+/* -log softmax(logits)[target]: the max in f32 (f32::max fold), exp of
+ * each (l - max) taken in f64 and summed in f64, the result cast to f32. */
+float tor_token_nll(const float *logits, size_t n, uint32_t target) {
+  float mx = -INFINITY;
+  for (size_t i = 0; i < n; ++i) mx = fmaxf(mx, logits[i]);
+  double sumexp = 0.0;
+  for (size_t i = 0; i < n; ++i) sumexp += exp((double)(logits[i] - mx));
+  const double log_prob = (double)(logits[target] - mx) - log(sumexp);
+  return (float)(-log_prob);
+}
+
 /* ------------------------------------------- GGUF, reader.rs:193-351 -- */
 
 enum { GT_U32 = 4, GT_I32 = 5, GT_F32 = 6, GT_BOOL = 7, GT_STR = 8, GT_ARR = 9 };

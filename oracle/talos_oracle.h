@@ -69,6 +69,9 @@ void tor_swiglu(const float *gate, const float *up, float *out, size_t n);
 void tor_rope(float *v, size_t pos, size_t n_head, size_t head_dim,
               float freq_base);
 uint32_t tor_argmax(const float *logits, size_t n);
+uint32_t tor_sample(const float *logits, size_t n, float temperature, size_t top_k, int has_top_p, float top_p,
+                    float u);
+float tor_token_nll(const float *logits, size_t n, uint32_t target);
 
 /* ---- GGUF v3 parse, src/gguf/reader.rs:193-351 ---- */
 typedef struct tor_gguf tor_gguf;

@@ -67,6 +67,11 @@ _SIGS = {
     "talos_hip_forward_token": (C.c_int, [_P, C.c_uint32, C.c_uint32, _F, _U32]),
     "talos_hip_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, _U32]),
     "talos_hip_kv_reset": (C.c_int, [_P]),
+    "talos_hip_sample": (C.c_int, [_P, C.c_float, C.c_uint32, C.c_float, C.c_float, _U32]),
+    "talos_hip_sample_dev": (C.c_int, [_P, _P, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_float, _P]),
+    "talos_hip_decode_sample": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32, C.c_float,
+                                          _F, _U32]),
+    "talos_hip_perplexity": (C.c_int, [_P, _U32, C.c_uint32, _F, _F]),
     "talos_hip_kv_read": (C.c_int, [_P, C.c_uint32, _F, _F]),
     "talos_hip_kv_write": (C.c_int, [_P, C.c_uint32, _F, _F]),
     "talos_hip_prefill": (C.c_int, [_P, _U32, C.c_uint32, C.c_uint32, _F, _U32]),
@@ -244,6 +249,14 @@ class HipBackend:
         b = C.c_double()
         self._check(lib().talos_hip_bench_matvec(self._h, arr, len(names), reps, C.byref(us), C.byref(b)))
         return us.value, b.value
+
+    def sample_dev(self, d_logits: int, n: int, d_token: int, temperature: float, top_k=None, top_p=None,
+                   u: float = 0.5):
+        """talos_hip_sample_dev on device pointers (enqueued, not waited for)."""
+        self._check(lib().talos_hip_sample_dev(self._h, C.c_void_p(d_logits), n, temperature,
+                                               0 if top_k is None else int(top_k),
+                                               float("inf") if top_p is None else float(top_p), u,
+                                               C.c_void_p(d_token)))
 
     def path(self) -> str:
         """The token step's implementation for the resident weights."""
@@ -438,6 +451,46 @@ class Model:
         self._check(lib().talos_model_prefill(self._h, _u32ptr(t), t.size, pos,
                                               _fptr(out) if out is not None else None, C.byref(am)))
         return out, am.value
+
+    @staticmethod
+    def _topp(top_p):
+        return float("inf") if top_p is None else float(top_p)
+
+    def sample(self, temperature: float, top_k=None, top_p=None, u: float = 0.5) -> int:
+        """Draw from the latest step's logits on the device (src/sample.rs:19-76;
+        u is the uniform draw)."""
+        t = C.c_uint32()
+        self._hip(lib().talos_hip_sample, temperature, 0 if top_k is None else int(top_k), self._topp(top_p), u,
+                  C.byref(t))
+        return t.value
+
+    def decode_sample(self, token: int, pos: int, u, temperature: float, top_k=None, top_p=None) -> np.ndarray:
+        """Sampled decode on the device: len(u) steps, draw s with u[s]."""
+        uu = np.ascontiguousarray(u, np.float32)
+        out = np.empty(max(uu.size, 1), np.uint32)
+        self._hip(lib().talos_hip_decode_sample, token, pos, uu.size, temperature,
+                  0 if top_k is None else int(top_k), self._topp(top_p), _fptr(uu), _u32ptr(out))
+        return out[: uu.size]
+
+    def perplexity(self, tokens):
+        """(perplexity, per-position NLLs) of teacher-forced tokens
+        (src/eval.rs:35-52) on the device."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        nll = np.empty(max(t.size - 1, 1), np.float32)
+        p = C.c_float()
+        self._hip(lib().talos_hip_perplexity, _u32ptr(t), t.size, C.byref(p), _fptr(nll))
+        ctx = self.cfg.context_length
+        scored = sum(min(ctx, t.size - c0) - 1 for c0 in range(0, t.size, ctx) if min(ctx, t.size - c0) >= 2)
+        return p.value, nll[:scored]
+
+    def sample_dev(self, d_logits: int, n: int, d_token: int, temperature: float, top_k=None, top_p=None,
+                   u: float = 0.5):
+        """talos_hip_sample_dev on device pointers (enqueued, not waited for)."""
+        self._hip(lib().talos_hip_sample_dev, C.c_void_p(d_logits), n, temperature,
+                  0 if top_k is None else int(top_k), self._topp(top_p), u, C.c_void_p(d_token))
+
+    def sync(self):
+        self._hip(lib().talos_hip_sync)
 
     def _hip(self, fn, *args):
         h = self.backend_handle()

@@ -20,6 +20,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -27,10 +28,12 @@
 #include "../../include/talos_hip.h"
 #include "mega.h"
 #include "mega_inst.h"
+#include "sample.h"
 
 namespace {
 
 std::string g_create_error;
+
 
 struct DevWeight {
   uint32_t type = 0;
@@ -78,6 +81,17 @@ struct talos_hip_ctx {
   float* uraw = nullptr;   // [n_ff]
   float* scores = nullptr; // [n_head][context_length]
   int path = TALOS_PATH_NONE;  // decided with the persistent-kernel set-up
+  // sampling workspace (k_sample): keys twice and the probabilities for up
+  // to samp_cap logits, the drawn token, the per-step draws and NLLs
+  uint64_t* samp_ka = nullptr;
+  uint64_t* samp_kb = nullptr;
+  float* samp_pb = nullptr;
+  uint32_t samp_cap = 0;
+  uint32_t* samp_out = nullptr;
+  float* samp_u = nullptr;
+  uint32_t samp_u_cap = 0;
+  float* nll = nullptr;
+  uint32_t nll_cap = 0;
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -859,6 +873,50 @@ int run_step(talos_hip_ctx* c, GraphKind kind, hipGraphExec_t g) {
   return TALOS_OK;
 }
 
+// Grow the sampling workspace to n logits.
+int samp_reserve(talos_hip_ctx* c, uint32_t n) {
+  if (!c->samp_out) HIPCHK(c, hipMalloc(&c->samp_out, 64));
+  if (c->samp_cap >= n) return TALOS_OK;
+  (void)hipStreamSynchronize(c->stream);
+  for (void* p : {(void*)c->samp_ka, (void*)c->samp_kb, (void*)c->samp_pb})
+    if (p) (void)hipFree(p);
+  c->samp_ka = c->samp_kb = nullptr;
+  c->samp_pb = nullptr;
+  c->samp_cap = 0;
+  HIPCHK(c, hipMalloc(&c->samp_ka, (size_t)n * 8));
+  HIPCHK(c, hipMalloc(&c->samp_kb, (size_t)n * 8));
+  HIPCHK(c, hipMalloc(&c->samp_pb, (size_t)n * 4));
+  c->samp_cap = n;
+  return TALOS_OK;
+}
+
+int samp_check(talos_hip_ctx* c, float temperature, float top_p, float u) {
+  if (std::isnan(temperature)) return fail(c, TALOS_ERR_ARG, "temperature is NaN");
+  if (!(u >= 0.f && u < 1.f)) return fail(c, TALOS_ERR_ARG, "u %g outside [0, 1)", (double)u);
+  (void)top_p;
+  return TALOS_OK;
+}
+
+void enq_sample(talos_hip_ctx* c, const float* logits, uint32_t n, float temperature, uint32_t top_k, float top_p,
+                float u, const float* u_dev, uint64_t* ka, uint64_t* kb, float* pb, uint32_t* out, int32_t* state,
+                int32_t* tokens) {
+  SampleArgs A{};
+  A.logits = logits;
+  A.n = n;
+  A.temperature = temperature;
+  A.top_k = top_k;
+  A.top_p = top_p;
+  A.u = u;
+  A.u_dev = u_dev;
+  A.ka = ka;
+  A.kb = kb;
+  A.pb = pb;
+  A.out = out;
+  A.state = state;
+  A.tokens = tokens;
+  hipLaunchKernelGGL(k_sample, dim3(1), dim3(SAMPLE_NT), 0, c->stream, A);
+}
+
 int check_ctx(talos_hip_ctx* c) {
   if (!c) return TALOS_ERR_ARG;
   c->err.clear();
@@ -947,6 +1005,7 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
     return fail(nullptr, TALOS_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
 
+
   // RoPE table, same expression as src/math/ops.rs:48-61 evaluated in f32
   // with the C library's powf/sinf/cosf.
   const uint32_t half = hd / 2;
@@ -976,6 +1035,7 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
+                 c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out, c->samp_u, c->nll,
                  c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart, c->qraw, c->kraw,
                  c->vraw, c->graw, c->uraw, c->scores};
   for (void* p : dev)
@@ -1162,6 +1222,140 @@ int talos_hip_prefill(talos_hip_ctx* c, const uint32_t* tokens, uint32_t n, uint
 }
 
 int talos_hip_kv_reset(talos_hip_ctx* c) { return check_ctx(c); }
+
+int talos_hip_sample(talos_hip_ctx* c, float temperature, uint32_t top_k, float top_p, float u, uint32_t* token) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!token) return fail(c, TALOS_ERR_ARG, "null token");
+  if ((rc = samp_check(c, temperature, top_p, u))) return rc;
+  if ((rc = set_device(c))) return rc;
+  if ((rc = alloc_acts(c))) return rc;
+  const uint32_t n = c->cfg.vocab_size;
+  if ((rc = samp_reserve(c, n))) return rc;
+  enq_sample(c, c->logits, n, temperature, top_k, top_p, u, nullptr, c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out,
+             nullptr, nullptr);
+  HIPCHK(c, hipGetLastError());
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->samp_out, 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  *token = (uint32_t)c->h_io[0];
+  return TALOS_OK;
+}
+
+int talos_hip_sample_dev(talos_hip_ctx* c, const float* d_logits, uint32_t n, float temperature, uint32_t top_k,
+                         float top_p, float u, uint32_t* d_token) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!d_logits || !d_token || n == 0) return fail(c, TALOS_ERR_ARG, "null logits or token, or n == 0");
+  if ((rc = samp_check(c, temperature, top_p, u))) return rc;
+  if ((rc = set_device(c))) return rc;
+  if ((rc = samp_reserve(c, n))) return rc;
+  enq_sample(c, d_logits, n, temperature, top_k, top_p, u, nullptr, c->samp_ka, c->samp_kb, c->samp_pb, d_token,
+             nullptr, nullptr);
+  HIPCHK(c, hipGetLastError());
+  return TALOS_OK;
+}
+
+int talos_hip_decode_sample(talos_hip_ctx* c, uint32_t token, uint32_t pos, uint32_t n_steps, float temperature,
+                            uint32_t top_k, float top_p, const float* u, uint32_t* tokens_out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (n_steps && (!tokens_out || !u)) return fail(c, TALOS_ERR_ARG, "null u or tokens_out");
+  if ((uint64_t)pos + n_steps > c->cfg.context_length)
+    return fail(c, TALOS_ERR_POS, "pos %u + %u steps exceeds context_length %u", pos, n_steps, c->cfg.context_length);
+  if (token >= c->cfg.vocab_size)
+    return fail(c, TALOS_ERR_TOKEN, "token %u >= vocab_size %u", token, c->cfg.vocab_size);
+  for (uint32_t s = 0; s < n_steps; ++s)
+    if ((rc = samp_check(c, temperature, top_p, u[s]))) return rc;
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_TOKEN, &g))) return rc;
+  const uint32_t n = c->cfg.vocab_size;
+  if ((rc = samp_reserve(c, n))) return rc;
+  if (c->samp_u_cap < n_steps) {
+    if (c->samp_u) (void)hipFree(c->samp_u);
+    c->samp_u = nullptr;
+    c->samp_u_cap = 0;
+    HIPCHK(c, hipMalloc(&c->samp_u, (size_t)std::max(n_steps, 1u) * 4));
+    c->samp_u_cap = std::max(n_steps, 1u);
+  }
+  if (n_steps) HIPCHK(c, hipMemcpyAsync(c->samp_u, u, (size_t)n_steps * 4, hipMemcpyHostToDevice, c->stream));
+  if ((rc = set_state(c, token, pos))) return rc;
+  // each step: the forward (its argmax is not used), then the draw, which
+  // sets the next token and advances the position on the device
+  for (uint32_t s = 0; s < n_steps; ++s) {
+    if ((rc = run_step(c, G_TOKEN, g))) return rc;
+    enq_sample(c, c->logits, n, temperature, top_k, top_p, 0.f, c->samp_u, c->samp_ka, c->samp_kb, c->samp_pb,
+               nullptr, c->io, c->tokens);
+  }
+  HIPCHK(c, hipGetLastError());
+  if (n_steps)
+    HIPCHK(c, hipMemcpyAsync(c->h_tokens, c->tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, hipStreamSynchronize(c->stream));
+  if ((rc = check_device_err(c))) return rc;
+  for (uint32_t s = 0; s < n_steps; ++s) tokens_out[s] = (uint32_t)c->h_tokens[s];
+  return TALOS_OK;
+}
+
+int talos_hip_perplexity(talos_hip_ctx* c, const uint32_t* tokens, uint32_t n, float* ppl, float* nll_out) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!tokens || !ppl) return fail(c, TALOS_ERR_ARG, "null tokens or ppl");
+  if (n < 2) return fail(c, TALOS_ERR_ARG, "perplexity needs at least 2 tokens, got %u", n);
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] >= c->cfg.vocab_size)
+      return fail(c, TALOS_ERR_TOKEN, "tokens[%u] = %u >= vocab_size %u", i, tokens[i], c->cfg.vocab_size);
+  if ((rc = set_device(c))) return rc;
+  hipGraphExec_t g;
+  if ((rc = get_graph(c, G_FEED, &g))) return rc;
+  const uint32_t ctx = c->cfg.context_length;
+  // scored positions: every chunk of ctx tokens with at least two scores
+  // its len - 1 next tokens (src/eval.rs:35-52)
+  uint32_t scored = 0;
+  for (uint32_t c0 = 0; c0 < n; c0 += ctx) {
+    const uint32_t len = std::min(ctx, n - c0);
+    if (len < 2) break;
+    scored += len - 1;
+  }
+  if (c->nll_cap < scored) {
+    if (c->nll) (void)hipFree(c->nll);
+    c->nll = nullptr;
+    c->nll_cap = 0;
+    HIPCHK(c, hipMalloc(&c->nll, (size_t)scored * 4));
+    c->nll_cap = scored;
+  }
+  uint32_t k = 0;
+  for (uint32_t c0 = 0; c0 < n; c0 += ctx) {
+    const uint32_t len = std::min(ctx, n - c0);
+    if (len < 2) break;
+    // a fresh cache per chunk (positions restart at 0; rows are
+    // position-indexed, so nothing needs clearing); the feed advances the
+    // position and takes each next input from the device copy
+    for (uint32_t i = 0; i < len; ++i) c->h_tokens[i] = (int32_t)tokens[c0 + i];
+    HIPCHK(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)len * 4, hipMemcpyHostToDevice, c->stream));
+    memset(c->h_io, 0, 64);
+    c->h_io[ST_TOKEN] = (int32_t)tokens[c0];
+    c->h_io[ST_NFEED] = (int32_t)len;
+    HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64, hipMemcpyHostToDevice, c->stream));
+    for (uint32_t i = 0; i + 1 < len; ++i) {
+      if ((rc = run_step(c, G_FEED, g))) return rc;
+      hipLaunchKernelGGL(k_nll, dim3(1), dim3(256), 0, c->stream, c->logits, c->cfg.vocab_size, tokens[c0 + i + 1],
+                         c->nll + k++);
+    }
+    // the host token buffer is reused by the next chunk
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+  }
+  HIPCHK(c, hipGetLastError());
+  std::vector<float> h(scored);
+  HIPCHK(c, hipMemcpy(h.data(), c->nll, (size_t)scored * 4, hipMemcpyDeviceToHost));
+  HIPCHK(c, hipMemcpy(c->h_io, c->io, 64, hipMemcpyDeviceToHost));
+  if ((rc = check_device_err(c))) return rc;
+  double sum = 0.0;
+  for (uint32_t i = 0; i < scored; ++i) sum += (double)h[i];
+  *ppl = (float)std::exp(sum / (double)scored);
+  if (nll_out) memcpy(nll_out, h.data(), (size_t)scored * 4);
+  return TALOS_OK;
+}
 
 int talos_hip_kv_read(talos_hip_ctx* c, uint32_t n_pos, float* k_out, float* v_out) {
   int rc;
