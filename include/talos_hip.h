@@ -143,6 +143,16 @@ int talos_hip_sample(talos_hip_ctx* ctx, float temperature, uint32_t top_k, floa
 int talos_hip_sample_dev(talos_hip_ctx* ctx, const float* d_logits, uint32_t n, float temperature, uint32_t top_k,
                          float top_p, float u, uint32_t* d_token);
 
+/* talos_hip_sample_dev without any allocation: the draw's workspace is a
+ * fixed scratch array in device memory that every GPU the library runs on
+ * holds for the life of the process (2.5 MB), so n is at most 131072
+ * (TALOS_ERR_SHAPE beyond).  It calls no hipMalloc/hipFree.  Calls that
+ * overlap on one GPU share that scratch and race; order them on one stream.
+ * No reference counterpart: for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it). */
+int talos_hip_sample_noalloc(talos_hip_ctx* ctx, const float* d_logits, uint32_t n, float temperature,
+                             uint32_t top_k, float top_p, float u, uint32_t* d_token);
+
 /* Sampled decode entirely on the device: starting from `token` at `pos`,
  * run n_steps forwards, each followed by a draw (as talos_hip_sample, with
  * draw u[s] for step s) that becomes the next input; writes the n_steps

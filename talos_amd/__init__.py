@@ -69,6 +69,7 @@ _SIGS = {
     "talos_hip_kv_reset": (C.c_int, [_P]),
     "talos_hip_sample": (C.c_int, [_P, C.c_float, C.c_uint32, C.c_float, C.c_float, _U32]),
     "talos_hip_sample_dev": (C.c_int, [_P, _P, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_float, _P]),
+    "talos_hip_sample_noalloc": (C.c_int, [_P, _P, C.c_uint32, C.c_float, C.c_uint32, C.c_float, C.c_float, _P]),
     "talos_hip_decode_sample": (C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32, C.c_float,
                                           _F, _U32]),
     "talos_hip_perplexity": (C.c_int, [_P, _U32, C.c_uint32, _F, _F]),
@@ -257,6 +258,15 @@ class HipBackend:
                                                0 if top_k is None else int(top_k),
                                                float("inf") if top_p is None else float(top_p), u,
                                                C.c_void_p(d_token)))
+
+    def sample_noalloc(self, d_logits: int, n: int, d_token: int, temperature: float, top_k=None, top_p=None,
+                       u: float = 0.5):
+        """talos_hip_sample_noalloc: the same draw with the library's fixed
+        scratch (no allocation; n <= 131072)."""
+        self._check(lib().talos_hip_sample_noalloc(self._h, C.c_void_p(d_logits), n, temperature,
+                                                   0 if top_k is None else int(top_k),
+                                                   float("inf") if top_p is None else float(top_p), u,
+                                                   C.c_void_p(d_token)))
 
     def path(self) -> str:
         """The token step's implementation for the resident weights."""

@@ -30,10 +30,36 @@
 #include "mega_inst.h"
 #include "sample.h"
 
+// Scratch of the allocation-free sampling entry point
+// (talos_hip_sample_noalloc): keys twice and the probabilities for up to
+// TALOS_SAMPLE_NOALLOC_MAX logits.  Each GPU holds its own copy for the life
+// of the process; host code reaches it only through the device address
+// hipGetSymbolAddress returns on that GPU.
+#define TALOS_SAMPLE_NOALLOC_MAX (1u << 17)
+static __device__ __align__(256) uint8_t scratch[(size_t)TALOS_SAMPLE_NOALLOC_MAX * 20];
+
 namespace {
 
 std::string g_create_error;
 
+std::mutex g_scratch_mu;
+std::vector<uint8_t*> g_scratch_ptr;  // per device ordinal, null until set up
+
+// With `dev` current: record this GPU's address of `scratch` (once).
+hipError_t scratch_setup(int dev) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (g_scratch_ptr[dev]) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e == hipSuccess) g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  return e;
+}
+
+uint8_t* scratch_ptr(int dev) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return dev < (int)g_scratch_ptr.size() ? g_scratch_ptr[dev] : nullptr;
+}
 
 struct DevWeight {
   uint32_t type = 0;
@@ -1004,6 +1030,12 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
                 c->max_lds);
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess)
     return fail(nullptr, TALOS_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  // this GPU's address of the allocation-free sampler's scratch (the
+  // device is current here)
+  if ((e = scratch_setup(f.device)) != hipSuccess) {
+    talos_hip_destroy(c.release());
+    return fail(nullptr, TALOS_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  }
 
 
   // RoPE table, same expression as src/math/ops.rs:48-61 evaluated in f32
@@ -1251,6 +1283,26 @@ int talos_hip_sample_dev(talos_hip_ctx* c, const float* d_logits, uint32_t n, fl
   if ((rc = samp_reserve(c, n))) return rc;
   enq_sample(c, d_logits, n, temperature, top_k, top_p, u, nullptr, c->samp_ka, c->samp_kb, c->samp_pb, d_token,
              nullptr, nullptr);
+  HIPCHK(c, hipGetLastError());
+  return TALOS_OK;
+}
+
+int talos_hip_sample_noalloc(talos_hip_ctx* c, const float* d_logits, uint32_t n, float temperature, uint32_t top_k,
+                             float top_p, float u, uint32_t* d_token) {
+  int rc;
+  if ((rc = check_ctx(c))) return rc;
+  if (!d_logits || !d_token || n == 0) return fail(c, TALOS_ERR_ARG, "null logits or token, or n == 0");
+  if (n > TALOS_SAMPLE_NOALLOC_MAX)
+    return fail(c, TALOS_ERR_SHAPE, "n %u exceeds the allocation-free sampler's maximum %u", n,
+                TALOS_SAMPLE_NOALLOC_MAX);
+  if ((rc = samp_check(c, temperature, top_p, u))) return rc;
+  if ((rc = set_device(c))) return rc;
+  uint8_t* sp = scratch_ptr(c->cfg.device);
+  if (!sp) return fail(c, TALOS_ERR_HIP, "sampling scratch of device %d not set up", c->cfg.device);
+  uint64_t* ka = reinterpret_cast<uint64_t*>(sp);
+  uint64_t* kb = reinterpret_cast<uint64_t*>(sp + (size_t)TALOS_SAMPLE_NOALLOC_MAX * 8);
+  float* pb = reinterpret_cast<float*>(sp + (size_t)TALOS_SAMPLE_NOALLOC_MAX * 16);
+  enq_sample(c, d_logits, n, temperature, top_k, top_p, u, nullptr, ka, kb, pb, d_token, nullptr, nullptr);
   HIPCHK(c, hipGetLastError());
   return TALOS_OK;
 }
