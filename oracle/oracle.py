@@ -14,6 +14,8 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "build", "libtalos_oracle.so")
+# the same source at -O3 -mavx2 (bit-identical results): the CPU baseline
+SIMD_LIB_PATH = os.path.join(HERE, "build", "libtalos_oracle_simd.so")
 
 F32, Q4_0, Q8_0, Q6_K = 0, 2, 8, 14
 _F = C.POINTER(C.c_float)
@@ -27,21 +29,31 @@ class Config(C.Structure):
                 ("rope_freq_base", C.c_float)]
 
 
-_lib = None
+_libs = {}
 
 
 def build() -> str:
-    """Compile the oracle with its Makefile (gcc)."""
+    """Compile the oracle with its Makefile (gcc): the parity build and the
+    AVX2 build."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
 
 
-def lib() -> C.CDLL:
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
+def host_has_avx2() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return any(line.startswith("flags") and " avx2" in line for line in f)
+    except OSError:
+        return False
+
+
+def lib(simd: bool = False) -> C.CDLL:
+    """The parity build, or (simd) the -O3 -mavx2 build of the same source."""
+    if simd not in _libs:
+        path = SIMD_LIB_PATH if simd else LIB_PATH
+        if not os.path.exists(path):
             build()
-        L = C.CDLL(LIB_PATH)
+        L = C.CDLL(path)
         sig = {
             "tor_f16_to_f32": (C.c_float, [C.c_uint16]),
             "tor_f32_to_f16": (C.c_uint16, [C.c_float]),
@@ -89,8 +101,8 @@ def lib() -> C.CDLL:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        _lib = L
-    return _lib
+        _libs[simd] = L
+    return _libs[simd]
 
 
 def _f(a):
@@ -222,7 +234,8 @@ class OracleModel:
     must outlive this object; pass (address, length) of memory the caller
     keeps alive, or a bytes object (kept referenced here)."""
 
-    def __init__(self, data, nthreads: int = 1):
+    def __init__(self, data, nthreads: int = 1, simd: bool = False):
+        self._L = lib(simd)
         if isinstance(data, (bytes, bytearray, np.ndarray)):
             self._keep = np.ascontiguousarray(np.frombuffer(data, np.uint8) if not isinstance(data, np.ndarray)
                                               else data, np.uint8)
@@ -231,52 +244,52 @@ class OracleModel:
             addr, n = data
             self._keep = None
         err = C.create_string_buffer(512)
-        h = lib().tor_model_load(C.c_void_p(addr), n, nthreads, err, 512)
+        h = self._L.tor_model_load(C.c_void_p(addr), n, nthreads, err, 512)
         if not h:
             raise RuntimeError(err.value.decode())
         self._h = h
         cfg = Config()
-        lib().tor_model_config(self._h, C.byref(cfg))
+        self._L.tor_model_config(self._h, C.byref(cfg))
         self.cfg = cfg
 
     def close(self):
         if getattr(self, "_h", None):
-            lib().tor_model_free(self._h)
+            self._L.tor_model_free(self._h)
             self._h = None
 
     __del__ = close
 
     def set_threads(self, n):
-        lib().tor_model_set_threads(self._h, n)
+        self._L.tor_model_set_threads(self._h, n)
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         out = np.empty(self.cfg.vocab_size, np.float32)
-        if lib().tor_model_forward(self._h, token, pos, _f(out)):
+        if self._L.tor_model_forward(self._h, token, pos, _f(out)):
             raise RuntimeError("oracle forward failed")
         return out
 
     def forward_hidden(self, token: int, pos: int) -> np.ndarray:
         out = np.empty(self.cfg.n_embd, np.float32)
-        if lib().tor_model_forward_hidden(self._h, token, pos, _f(out)):
+        if self._L.tor_model_forward_hidden(self._h, token, pos, _f(out)):
             raise RuntimeError("oracle forward failed")
         return out
 
     def reset(self):
-        lib().tor_model_reset(self._h)
+        self._L.tor_model_reset(self._h)
 
     def cap_context(self, n):
-        lib().tor_model_cap_context(self._h, n)
+        self._L.tor_model_cap_context(self._h, n)
         cfg = Config()
-        lib().tor_model_config(self._h, C.byref(cfg))
+        self._L.tor_model_config(self._h, C.byref(cfg))
         self.cfg = cfg
 
     def kv_len(self) -> int:
-        return lib().tor_model_kv_len(self._h)
+        return self._L.tor_model_kv_len(self._h)
 
     def set_kv(self, k: np.ndarray, v: np.ndarray):
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
-        lib().tor_model_set_kv(self._h, _f(k), _f(v), k.shape[1])
+        self._L.tor_model_set_kv(self._h, _f(k), _f(v), k.shape[1])
 
     def get_kv(self, n_pos: int):
         """K and V of the first n_pos cached positions, [layer, pos, kv_dim]."""
@@ -284,7 +297,7 @@ class OracleModel:
         kvd = c.n_head_kv * (c.n_embd // c.n_head)
         k = np.empty((c.n_layer, n_pos, kvd), np.float32)
         v = np.empty_like(k)
-        if lib().tor_model_get_kv(self._h, _f(k), _f(v), n_pos) != 0:
+        if self._L.tor_model_get_kv(self._h, _f(k), _f(v), n_pos) != 0:
             raise ValueError(f"only {self.kv_len()} positions cached")
         return k, v
 

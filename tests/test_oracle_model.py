@@ -295,3 +295,38 @@ def test_kv_injection_resumes_the_forward():
         a.get_kv(99)
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("qtype", [O.F32, O.Q8_0, O.Q4_0])
+def test_simd_build_is_bit_identical(qtype):
+    """The CPU baseline's -O3 -mavx2 build of the oracle gives the parity
+    build's logits bit for bit (no FMA contraction, no reassociation)."""
+    if not O.host_has_avx2():
+        pytest.skip("host has no AVX2")
+    rng = np.random.default_rng(41 + qtype)
+    W = rand_model(rng, **SHAPE, scale=0.3)
+    data = gguf_of(W, **SHAPE, qtype=qtype)
+    a = O.OracleModel(data, nthreads=4)
+    b = O.OracleModel(data, nthreads=4, simd=True)
+    for pos, t in enumerate([3, 1, 4, 1, 5, 9, 2, 6]):
+        la, lb = a.forward(t, pos), b.forward(t, pos)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), f"pos {pos}"
+    a.close()
+    b.close()
+
+
+def test_simd_build_is_bit_identical_q6k_output():
+    from tests import models as MB
+    shape = dict(embd=256, n_head=4, n_head_kv=2, ff=512, vocab=300, n_layer=1)
+    W = MB.normal_model(8, **shape)
+    types = {n: 2 for n in MB.layer_names(1)}
+    types["output.weight"] = 14
+    data = MB.gguf_bytes(W, ctx=16, types=types, **shape)
+    if not O.host_has_avx2():
+        pytest.skip("host has no AVX2")
+    a = O.OracleModel(data, nthreads=4)
+    b = O.OracleModel(data, nthreads=4, simd=True)
+    for pos, t in enumerate([3, 1, 4, 1]):
+        assert np.array_equal(a.forward(t, pos).view(np.uint32), b.forward(t, pos).view(np.uint32))
+    a.close()
+    b.close()
