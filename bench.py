@@ -19,8 +19,8 @@ tokens are also compared with the GPU's.
 
 The default run also reports, after the headline line's own measurements,
 `small_models` (tok/s of the tiny F32 and GQA Q8_0 models) and `lc` (the
-long-context case below with a seeded K/V state, its decode tok/s and
-roofline); --no-extra skips them.  `parity` records the GPU/CPU comparison
+long-context case below: its prompt tok/s, decode tok/s and roofline);
+--no-extra skips them.  `parity` records the GPU/CPU comparison
 of the CPU baseline's sample (greedy tokens and worst max-abs logit
 difference); a failed comparison makes the run exit with status 3.
 
@@ -337,10 +337,11 @@ def small_models() -> dict:
 
 
 def lc_measure(args) -> dict:
-    """The long-context case beside the headline one: the 7B shape in Q8_0
-    with a seeded K/V state of 16384 positions written to the cache, then 64
-    greedy steps (decode tok/s and the step's roofline at the middle
-    position).  Its parity is the GPU tests' (tests/test_gpu_long.py)."""
+    """The long-context case beside the headline one: the 7B shape in Q8_0,
+    its cache filled to 16384 positions by talos_hip_prefill of a uniform
+    random prefix (timed: prompt tok/s), then 64 greedy steps (decode tok/s
+    and the step's roofline at the middle position).  Its parity is the GPU
+    tests' (tests/test_gpu_long.py, tests/test_gpu_prefill.py)."""
     import numpy as np
 
     import talos_amd as T
@@ -351,13 +352,13 @@ def lc_measure(args) -> dict:
     t = time.perf_counter()
     model = T.Model.synth(spec, nthreads=nthreads)
     rng = np.random.default_rng(spec.seed + 1)
-    model.forward_token(1, 0, want_logits=False)  # uploads the weights
-    k = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)
-    v = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)
-    model.kv_write(k, v)
-    del k, v
-    log(f"lc: model and {P}-position cache ready in {time.perf_counter() - t:.1f}s")
-    first = int(rng.integers(0, spec.vocab_size))
+    prefix = rng.integers(0, spec.vocab_size, P).astype(np.uint32)
+    model.prefill(prefix[:64], 0, want_logits=False)  # uploads the weights, sizes the batch buffers
+    log(f"lc: model ready in {time.perf_counter() - t:.1f}s")
+    t = time.perf_counter()
+    _, first = model.prefill(prefix, 0, want_logits=False)
+    prefill_s = time.perf_counter() - t
+    log(f"lc: prefill of {P} positions {prefill_s:.2f}s ({P / prefill_s:.0f} tok/s)")
     model.decode_greedy(first, P, 8)
     t0 = time.perf_counter()
     toks = model.decode_greedy(first, P, steps)
@@ -369,8 +370,9 @@ def lc_measure(args) -> dict:
     kvpos = configs.kv_bytes_per_position(spec)
     tok_bytes = wbytes + kvpos * (P + (steps + 1) / 2.0) + kvpos
     model.close()
-    res = {"workload": f"mistral7b_q8_long: 7B shape, Q8_0 matrices, seeded K/V state of {P} positions, "
-                       f"{steps} greedy steps", "tok_s": round(steps / dt, 2), "steps": steps,
+    res = {"workload": f"mistral7b_q8_long: 7B shape, Q8_0 matrices, {P}-token uniform random prompt "
+                       f"(talos_hip_prefill), {steps} greedy steps", "tok_s": round(steps / dt, 2), "steps": steps,
+           "prefill_tok_s": round(P / prefill_s, 1),
            "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(k_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": int(sbytes),
                         "us_per_launch": round(us, 2), "pos": mid},
@@ -415,7 +417,7 @@ def run_lc(args) -> int:
             _, first = model.prefill(prefix[i:i + chunk], i, want_logits=False)
             log(f"  prefill {min(i + chunk, P)}/{P} positions, {time.perf_counter() - t:.1f}s")
         prefill_tok_s = P / (time.perf_counter() - t)
-        fill = f"device prompt feed of a uniform random {P}-token prefix ({prefill_tok_s:.1f} tok/s)"
+        fill = f"talos_hip_prefill of a uniform random {P}-token prefix ({prefill_tok_s:.1f} tok/s)"
     else:
         k = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)
         v = rng.standard_normal((spec.n_layer, P, spec.kv_dim), dtype=np.float32) * np.float32(1.28)

@@ -1,0 +1,292 @@
+// prefill.h -- batched prompt processing on the matrix cores.
+//
+// The reference feeds a prompt one Model::step per token (src/main.rs:
+// 88-94).  Here a chunk of T prompt tokens goes through each layer together
+// (src/model/llama.rs:96-176 for T rows at once), so every weight byte is
+// read once per chunk instead of once per token:
+//   rows: x_t = dequant_row(token_embd, tok_t); per layer
+//   rmsnorm -> q, k, v = GEMMs -> RoPE, K/V rows into the cache ->
+//   causal attention -> x += GEMM(o) -> rmsnorm -> gate, up = GEMMs ->
+//   SwiGLU -> x += GEMM(down).
+// The GEMMs run on v_mfma_f32_16x16x4_f32 (f32 products and sums, the
+// dequantized weight in f32: exactly the weight the reference multiplies),
+// the attention as a flash-style loop on the same instruction.  Only the
+// chunk's last row goes on to the final norm and the output projection.
+//
+// v_mfma_f32_16x16x4_f32 (one wave): D[16][16] += A[16][4] B[4][16] with
+// lane l supplying A[l % 16][l / 16] and B[l / 16][l % 16], and holding
+// D[4 (l / 16) + r][l % 16] in result register r (checked on the device).
+#pragma once
+#include "kernels.h"
+
+typedef float pf4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ pf4 mfma16x4(float a, float b, pf4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// x_t = dequant_row(token_embd, tok_t) (src/model/weights.rs:58-62).
+__global__ __launch_bounds__(256) void k_pf_embed(DevMat M, const int32_t* __restrict__ toks, uint32_t n,
+                                                  float* __restrict__ X) {
+  const uint32_t t = blockIdx.x, tok = (uint32_t)toks[t];
+  for (uint32_t e = threadIdx.x; e < n; e += 256) X[(size_t)t * n + e] = dq_elem(M, tok, e);
+}
+
+// Xn_t = rmsnorm(x_t) * w (src/math/ops.rs:5-12), one row per block.
+__global__ __launch_bounds__(256) void k_pf_rmsnorm(const float* __restrict__ X, const float* __restrict__ w,
+                                                    float eps, uint32_t n, float* __restrict__ Xn) {
+  __shared__ float red[8];
+  const float* x = X + (size_t)blockIdx.x * n;
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) ss += x[i] * x[i];
+  ss = block_sum(ss, red, 4);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+  for (uint32_t i = threadIdx.x; i < n; i += 256) Xn[(size_t)blockIdx.x * n + i] = x[i] * scale * w[i];
+}
+
+// ------------------------------------------------------------- the GEMM --
+// Y[t][r] (+)= sum_k Xn[t][k] W[r][k] for t < T, r < M (Y's row pitch ldy).
+// Block: 4 waves, a tile of 64 tokens x 64 rows; wave w owns rows
+// [64 bx + 16 w, +16) for all 64 tokens (four 16 x 16 MFMA tiles).  Per
+// 64-wide K chunk the block stages Xn transposed in LDS, [k][token] with a
+// pitch of 80 floats (the 64 lanes of one A read hit 64 distinct banks);
+// each lane dequantizes its weight row's elements k = 4 s + l / 16 of every
+// 32-element block straight from the repacked layout.
+#define PF_KC 64
+#define PF_AP 80
+
+struct PfGemm {
+  DevMat W;
+  const float* X;   // [T][K]
+  float* Y;         // [T][ldy]
+  uint32_t T, K, M, ldy;
+  int accumulate;
+};
+
+template <uint32_t FMT>
+__global__ __launch_bounds__(256) void k_pf_gemm(PfGemm G) {
+  __shared__ float As[PF_KC * PF_AP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const uint32_t tb = blockIdx.y * 64;
+  const uint32_t row = blockIdx.x * 64 + wave * 16 + li;
+  const uint32_t rowc = row < G.M ? row : G.M - 1;
+  pf4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = pf4{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t k0 = 0; k0 < G.K; k0 += PF_KC) {
+    // stage Xn[tb .. +64][k0 .. +64] transposed (zeros past T and K)
+    __syncthreads();
+    for (int i = tid; i < 64 * PF_KC; i += 256) {
+      const int tt = i / PF_KC, kk = i % PF_KC;
+      const uint32_t t = tb + tt, k = k0 + kk;
+      As[kk * PF_AP + tt] = (t < G.T && k < G.K) ? G.X[(size_t)t * G.K + k] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int blk = 0; blk < PF_KC / 32; ++blk) {
+      const uint32_t kb = k0 + blk * 32;  // this 32-element block of K
+      float b[8];                         // W[row][kb + 4 s + g], s = 0..7
+      if constexpr (FMT == TALOS_FMT_Q4_0) {
+        const uint32_t nb = G.K / 32, bi = kb / 32 < nb ? kb / 32 : nb - 1;
+        const size_t ci = (size_t)rowc * nb + bi;
+        const u4 q = *reinterpret_cast<const u4*>(G.W.q + ci * 16);
+        const float d = f16_to_f32(G.W.d[ci]);
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+        // element e = 4 s + g: byte e & 15, low nibble for e < 16
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int e = 4 * s + g, by = e & 15;
+          const uint32_t v = (w4[by >> 2] >> (8 * (by & 3))) & 0xFFu;
+          const int nib = e < 16 ? (int)(v & 15u) : (int)(v >> 4);
+          b[s] = (kb < G.K) ? d * (float)(nib - 8) : 0.f;
+        }
+      } else if constexpr (FMT == TALOS_FMT_Q8_0) {
+        const uint32_t nb = G.K / 32, bi = kb / 32 < nb ? kb / 32 : nb - 1;
+        const size_t ci = (size_t)rowc * nb + bi;
+        const u4 q0 = *reinterpret_cast<const u4*>(G.W.q + ci * 32);
+        const u4 q1 = *reinterpret_cast<const u4*>(G.W.q + ci * 32 + 16);
+        const float d = f16_to_f32(G.W.d[ci]);
+        const uint32_t w8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int e = 4 * s + g;
+          const uint32_t v = ((w8[e >> 2] >> (8 * (e & 3))) & 0xFFu) ^ 0x80u;
+          b[s] = (kb < G.K) ? d * (float)(int8_t)v : 0.f;
+        }
+      } else {  // F32: rows padded to nchunk * 4 floats
+        const float* wr = reinterpret_cast<const float*>(G.W.q) + (size_t)rowc * G.W.nchunk * 4;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t k = kb + 4 * s + g;
+          b[s] = k < G.K ? wr[k] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int kk = blk * 32 + 4 * s + g;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16x4(As[kk * PF_AP + 16 * t + li], b[s], acc[t]);
+      }
+    }
+  }
+  // D[4 g + r][li] of tile t: token tb + 16 t + 4 g + r, weight row `row`
+  if (row < G.M) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t tok = tb + 16 * t + 4 * g + r;
+        if (tok < G.T) {
+          float* y = G.Y + (size_t)tok * G.ldy + row;
+          *y = G.accumulate ? *y + acc[t][r] : acc[t][r];
+        }
+      }
+  }
+}
+
+// RoPE of the raw q and k rows of T tokens at positions p0 + t (any
+// head_dim, as k_rope_qkv), the K and V rows into the cache.
+__global__ __launch_bounds__(256) void k_pf_rope_kv(const float* __restrict__ Qr, const float* __restrict__ Kr,
+                                                    const float* __restrict__ Vr, float* __restrict__ Q,
+                                                    float* __restrict__ kc, float* __restrict__ vc,
+                                                    const float* __restrict__ rope, uint32_t p0, uint32_t n,
+                                                    uint32_t n_head, uint32_t hd, uint32_t kv_dim) {
+  const uint32_t t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  const int pos = (int)(p0 + t);
+  if (i < n) Q[(size_t)t * n + i] = i < n_head * hd ? rope_elem(Qr + (size_t)t * n, i, hd, pos, rope) : Qr[(size_t)t * n + i];
+  if (i < kv_dim) {
+    kc[(size_t)pos * kv_dim + i] = rope_elem(Kr + (size_t)t * kv_dim, i, hd, pos, rope);
+    vc[(size_t)pos * kv_dim + i] = Vr[(size_t)t * kv_dim + i];
+  }
+}
+
+// h = silu(g) * u row-wise over T rows of ff (src/math/ops.rs:28-37).
+__global__ __launch_bounds__(256) void k_pf_swiglu(const float* __restrict__ Gt, const float* __restrict__ Ut,
+                                                   float* __restrict__ H, size_t count) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) H[i] = (Gt[i] / (1.0f + expf(-Gt[i]))) * Ut[i];
+}
+
+// ---------------------------------------------------- flash attention --
+// ATT[t][h hd ..] = softmax_j(<q_t,h, K_j> / sqrt(hd)) V_j over positions
+// j <= p0 + t (src/model/llama.rs:135-155 for T queries).  Block: KV head
+// kvh, 16 queries, one wave per q head of the group (HPB waves); K/V tiles of
+// 64 positions staged in LDS and shared by the waves.  Per wave and tile:
+//   S^T = K Q^T on the matrix cores, the K rows of each 16-position
+//   sub-tile taken in the order pi(i) = 4 (i % 4) + i / 4, so that result
+//   register r of lane l holds position 4 r + l / 16 for query l % 16 --
+//   exactly the B operand of step r of the next product;
+//   online softmax per query in log2 units;
+//   O^T += V^T P^T on the matrix cores (hd / 16 tiles of 16 dimensions).
+// Requires head_dim % 16 == 0 (<= 256) and a group of at most 8 (waves).
+#define PF_ATT_Q 16
+#define PF_ATT_KT 64
+
+struct PfAttn {
+  const float* Q;    // [T][n] (rotated)
+  const float* kc;   // this layer's cache [ctx][kv_dim]
+  const float* vc;
+  float* out;        // [T][n]
+  uint32_t T, p0, n, kv_dim, hd, group;
+  float scale;       // 1 / sqrt(hd)
+};
+
+template <int HD>
+__global__ __launch_bounds__(512) void k_pf_attn(PfAttn A) {
+  constexpr int KP = HD + 4, VP = HD + 16;  // LDS pitches: conflict-free A reads of K and of V
+  extern __shared__ float sm[];
+  float* Ks = sm;                   // [64][KP]
+  float* Vs = sm + PF_ATT_KT * KP;  // [64][VP]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * PF_ATT_Q;
+  const uint32_t h = kvh * A.group + (uint32_t)wave;  // this wave's q head
+  const bool live = (uint32_t)wave < A.group;
+  const uint32_t tq = t0 + li;                         // this lane's query (B column)
+  const int qpos = (int)(A.p0 + (tq < A.T ? tq : A.T - 1));
+  constexpr float kLog2e = 1.4426950408889634f;
+  // Q^T fragments: lane l supplies Q[query li][d = 4 s + g] for step s
+  float qf[HD / 4];
+  {
+    const float* qrow = A.Q + (size_t)(tq < A.T ? tq : A.T - 1) * A.n + (size_t)(live ? h : 0) * HD;
+#pragma unroll
+    for (int s = 0; s < HD / 4; ++s) qf[s] = qrow[4 * s + g] * (A.scale * kLog2e);
+  }
+  pf4 o[HD / 16];
+#pragma unroll
+  for (int i = 0; i < HD / 16; ++i) o[i] = pf4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  // positions 0 .. last, last = the block's largest query position
+  const int last = (int)(A.p0 + min(t0 + PF_ATT_Q, A.T) - 1);
+  const int nthreads = blockDim.x;
+  for (int j0 = 0; j0 <= last; j0 += PF_ATT_KT) {
+    __syncthreads();
+    for (int i = tid; i < PF_ATT_KT * HD; i += nthreads) {
+      const int pj = i / HD, d = i % HD, j = j0 + pj;
+      const bool ok = j <= last;
+      Ks[pj * KP + d] = ok ? A.kc[(size_t)j * A.kv_dim + (size_t)kvh * HD + d] : 0.f;
+      Vs[pj * VP + d] = ok ? A.vc[(size_t)j * A.kv_dim + (size_t)kvh * HD + d] : 0.f;
+    }
+    __syncthreads();
+    if (!live) continue;
+    // S^T for the four 16-position sub-tiles
+    pf4 st[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      st[u] = pf4{0.f, 0.f, 0.f, 0.f};
+      const int prow = 16 * u + 4 * (li % 4) + li / 4;  // pi(li) within sub-tile u
+#pragma unroll
+      for (int s = 0; s < HD / 4; ++s) st[u] = mfma16x4(Ks[prow * KP + 4 * s + g], qf[s], st[u]);
+    }
+    // causal mask and the tile's max per query (lanes li, li+16, li+32, li+48)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j0 + 16 * u + 4 * r + g;
+        if (j > qpos) st[u][r] = -INFINITY;
+        mx = fmaxf(mx, st[u][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = st[u][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[u][r] - mn);
+        st[u][r] = p;
+        ps += p;
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i) o[i] *= alpha;
+    // O^T[dim][query] += V^T P^T: step r of sub-tile u covers positions
+    // 16 u + 4 r + (0..3); lane l supplies V[16 u + 4 r + g][16 i + li] and
+    // P[query li][16 u + 4 r + g] = st[u][r]
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pj = 16 * u + 4 * r + g;
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) o[i] = mfma16x4(Vs[pj * VP + 16 * i + li], st[u][r], o[i]);
+      }
+  }
+  // O^T tile i, register r: dim 16 i + 4 g + r of query li
+  if (live && tq < A.T) {
+    const float inv = 1.0f / l;
+    float* dst = A.out + (size_t)tq * A.n + (size_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[16 * i + 4 * g + r] = o[i][r] * inv;
+  }
+}

@@ -29,6 +29,7 @@
 #include "mega.h"
 #include "mega_inst.h"
 #include "sample.h"
+#include "prefill.h"
 
 // Scratch of the allocation-free sampling entry point
 // (talos_hip_sample_noalloc): keys twice and the probabilities for up to
@@ -118,6 +119,12 @@ struct talos_hip_ctx {
   uint32_t samp_u_cap = 0;
   float* nll = nullptr;
   uint32_t nll_cap = 0;
+  // batched prompt processing (prefill.h): chunk buffers of pf_cap rows
+  uint32_t pf_cap = 0;
+  float *pf_x = nullptr, *pf_xn = nullptr, *pf_qr = nullptr, *pf_q = nullptr, *pf_att = nullptr;
+  float *pf_kr = nullptr, *pf_vr = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_h = nullptr;
+  int32_t* pf_tok = nullptr;
+  bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -943,6 +950,136 @@ void enq_sample(talos_hip_ctx* c, const float* logits, uint32_t n, float tempera
   hipLaunchKernelGGL(k_sample, dim3(1), dim3(SAMPLE_NT), 0, c->stream, A);
 }
 
+// ---- batched prompt processing (prefill.h)
+
+#define PF_CHUNK 1024
+
+// The batched path takes layers whose matrices are F32, Q4_0 or Q8_0 and
+// attention heads of a multiple of 16 up to 256 that tile n_embd exactly,
+// with groups of at most 8.
+int pf_supported(talos_hip_ctx* c, bool* ok) {
+  *ok = false;
+  if (!c->allow_batch || c->hd % 16 || c->hd > 256 || c->group > 8 || c->cfg.n_embd != c->cfg.n_head * c->hd)
+    return TALOS_OK;
+  for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
+    LayerW w;
+    int rc = layer_weights(c, l, &w);
+    if (rc) return rc;
+    for (const DevWeight* m : {w.q, w.k, w.v, w.o, w.g, w.u, w.d})
+      if (m->type == TALOS_GGML_Q6_K) return TALOS_OK;
+  }
+  const size_t lds = (size_t)PF_ATT_KT * (2 * c->hd + 20) * 4;
+  *ok = lds <= c->max_lds;
+  return TALOS_OK;
+}
+
+int pf_reserve(talos_hip_ctx* c, uint32_t T) {
+  if (c->pf_cap >= T) return TALOS_OK;
+  (void)hipStreamSynchronize(c->stream);
+  for (float** p : {&c->pf_x, &c->pf_xn, &c->pf_qr, &c->pf_q, &c->pf_att, &c->pf_kr, &c->pf_vr, &c->pf_g, &c->pf_u,
+                    &c->pf_h}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
+  if (c->pf_tok) (void)hipFree(c->pf_tok);
+  c->pf_tok = nullptr;
+  c->pf_cap = 0;
+  const size_t n = c->cfg.n_embd, kv = c->kv_dim, ff = c->cfg.n_ff;
+  for (float** p : {&c->pf_x, &c->pf_xn, &c->pf_qr, &c->pf_q, &c->pf_att}) HIPCHK(c, hipMalloc(p, (size_t)T * n * 4));
+  for (float** p : {&c->pf_kr, &c->pf_vr}) HIPCHK(c, hipMalloc(p, (size_t)T * kv * 4));
+  for (float** p : {&c->pf_g, &c->pf_u, &c->pf_h}) HIPCHK(c, hipMalloc(p, (size_t)T * ff * 4));
+  HIPCHK(c, hipMalloc(&c->pf_tok, (size_t)T * 4));
+  c->pf_cap = T;
+  return TALOS_OK;
+}
+
+// Y[T][ldy] (+)= X[T][w.cols] W^T
+void enq_gemm(talos_hip_ctx* c, const DevWeight* w, const float* X, uint32_t T, float* Y, uint32_t ldy, int acc) {
+  PfGemm G{};
+  G.W = w->mat;
+  G.X = X;
+  G.Y = Y;
+  G.T = T;
+  G.K = (uint32_t)w->cols;
+  G.M = (uint32_t)w->rows;
+  G.ldy = ldy;
+  G.accumulate = acc;
+  const dim3 grid((G.M + 63) / 64, (T + 63) / 64);
+  switch (w->type) {
+    case TALOS_GGML_Q4_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(256), 0, c->stream, G); break;
+    case TALOS_GGML_Q8_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(256), 0, c->stream, G); break;
+    default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(256), 0, c->stream, G); break;
+  }
+}
+
+void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
+  PfAttn A{};
+  A.Q = c->pf_q;
+  A.kc = c->kc[l];
+  A.vc = c->vc[l];
+  A.out = c->pf_att;
+  A.T = T;
+  A.p0 = p0;
+  A.n = c->cfg.n_embd;
+  A.kv_dim = c->kv_dim;
+  A.hd = c->hd;
+  A.group = c->group;
+  A.scale = 1.0f / sqrtf((float)c->hd);
+  const dim3 grid(c->cfg.n_head_kv, (T + PF_ATT_Q - 1) / PF_ATT_Q), block(64 * c->group);
+  const size_t lds = (size_t)PF_ATT_KT * (2 * c->hd + 20) * 4;
+  switch (c->hd / 16) {
+#define PF_ATT_CASE(N) \
+  case N: hipLaunchKernelGGL(k_pf_attn<16 * N>, grid, block, lds, c->stream, A); break;
+    PF_ATT_CASE(1) PF_ATT_CASE(2) PF_ATT_CASE(3) PF_ATT_CASE(4) PF_ATT_CASE(5) PF_ATT_CASE(6) PF_ATT_CASE(7)
+    PF_ATT_CASE(8) PF_ATT_CASE(9) PF_ATT_CASE(10) PF_ATT_CASE(11) PF_ATT_CASE(12) PF_ATT_CASE(13) PF_ATT_CASE(14)
+    PF_ATT_CASE(15) PF_ATT_CASE(16)
+#undef PF_ATT_CASE
+    default: break;
+  }
+}
+
+void set_pf_attn_lds(int bytes) {
+#define PF_ATT_SET(N) set_max_lds((const void*)k_pf_attn<16 * N>, bytes);
+  PF_ATT_SET(1) PF_ATT_SET(2) PF_ATT_SET(3) PF_ATT_SET(4) PF_ATT_SET(5) PF_ATT_SET(6) PF_ATT_SET(7) PF_ATT_SET(8)
+  PF_ATT_SET(9) PF_ATT_SET(10) PF_ATT_SET(11) PF_ATT_SET(12) PF_ATT_SET(13) PF_ATT_SET(14) PF_ATT_SET(15)
+  PF_ATT_SET(16)
+#undef PF_ATT_SET
+}
+
+// One chunk of T prompt tokens at positions p0 .. p0 + T - 1 through every
+// layer; leaves the chunk's rows in pf_x.
+int pf_chunk(talos_hip_ctx* c, const uint32_t* tokens, uint32_t T, uint32_t p0) {
+  const auto& cf = c->cfg;
+  const uint32_t n = cf.n_embd, kv = c->kv_dim, ff = cf.n_ff;
+  int rc;
+  const DevWeight* emb;
+  if ((rc = need_matrix(c, "token_embd.weight", cf.vocab_size, n, &emb))) return rc;
+  for (uint32_t i = 0; i < T; ++i) c->h_tokens[i] = (int32_t)tokens[i];
+  HIPCHK(c, hipMemcpyAsync(c->pf_tok, c->h_tokens, (size_t)T * 4, hipMemcpyHostToDevice, c->stream));
+  hipLaunchKernelGGL(k_pf_embed, dim3(T), dim3(256), 0, c->stream, emb->mat, c->pf_tok, n, c->pf_x);
+  for (uint32_t l = 0; l < cf.n_layer; ++l) {
+    LayerW w;
+    if ((rc = layer_weights(c, l, &w))) return rc;
+    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.an, cf.rms_eps, n, c->pf_xn);
+    enq_gemm(c, w.q, c->pf_xn, T, c->pf_qr, n, 0);
+    enq_gemm(c, w.k, c->pf_xn, T, c->pf_kr, kv, 0);
+    enq_gemm(c, w.v, c->pf_xn, T, c->pf_vr, kv, 0);
+    hipLaunchKernelGGL(k_pf_rope_kv, dim3((std::max(n, kv) + 255) / 256, T), dim3(256), 0, c->stream, c->pf_qr,
+                       c->pf_kr, c->pf_vr, c->pf_q, c->kc[l], c->vc[l], c->rope, p0, n, cf.n_head, c->hd, kv);
+    enq_pf_attn(c, l, T, p0);
+    enq_gemm(c, w.o, c->pf_att, T, c->pf_x, n, 1);
+    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.fn, cf.rms_eps, n, c->pf_xn);
+    enq_gemm(c, w.g, c->pf_xn, T, c->pf_g, ff, 0);
+    enq_gemm(c, w.u, c->pf_xn, T, c->pf_u, ff, 0);
+    const size_t cnt = (size_t)T * ff;
+    hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, c->stream, c->pf_g, c->pf_u,
+                       c->pf_h, cnt);
+    enq_gemm(c, w.d, c->pf_h, T, c->pf_x, n, 1);
+  }
+  HIPCHK(c, hipGetLastError());
+  return TALOS_OK;
+}
+
 int check_ctx(talos_hip_ctx* c) {
   if (!c) return TALOS_ERR_ARG;
   c->err.clear();
@@ -995,6 +1132,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_attn_wait = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_DSPLIT");
   c->allow_dsplit = env && (env[0] == '0' || env[0] == '1') ? env[0] - '0' : 2;
+  env = getenv("TALOS_HIP_BATCH");
+  c->allow_batch = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
@@ -1022,6 +1161,7 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   set_lds_attr_fmt<TALOS_FMT_Q4_0>((int)c->max_lds);
   set_lds_attr_fmt<TALOS_FMT_Q8_0>((int)c->max_lds);
   set_lds_attr_fmt<TALOS_FMT_Q6_K>((int)c->max_lds);
+  set_pf_attn_lds((int)c->max_lds);
   for (const void* k : {(const void*)k_attn_scores, (const void*)k_attn<2>, (const void*)k_attn<3>, (const void*)k_attn<4>,
                         (const void*)k_attn<5>, (const void*)k_attn<6>, (const void*)k_attn<7>, (const void*)k_attn<8>})
     set_max_lds(k, (int)c->max_lds);
@@ -1067,7 +1207,8 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
-                 c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out, c->samp_u, c->nll,
+                 c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out, c->samp_u, c->nll, c->pf_x, c->pf_xn,
+                 c->pf_qr, c->pf_q, c->pf_att, c->pf_kr, c->pf_vr, c->pf_g, c->pf_u, c->pf_h, c->pf_tok,
                  c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart, c->qraw, c->kraw,
                  c->vraw, c->graw, c->uraw, c->scores};
   for (void* p : dev)
@@ -1234,6 +1375,43 @@ int talos_hip_prefill(talos_hip_ctx* c, const uint32_t* tokens, uint32_t n, uint
   if ((rc = set_device(c))) return rc;
   hipGraphExec_t g;
   if ((rc = get_graph(c, G_FEED, &g))) return rc;
+  bool batched = false;
+  if ((rc = pf_supported(c, &batched))) return rc;
+  if (batched) {
+    // chunks of up to PF_CHUNK tokens through every layer at once; the last
+    // token's row then takes the final norm, the output projection and the
+    // argmax as a decode step's head does
+    if ((rc = pf_reserve(c, std::min(n, (uint32_t)PF_CHUNK)))) return rc;
+    uint32_t last = 0;
+    for (uint32_t c0 = 0; c0 < n; c0 += PF_CHUNK) {
+      const uint32_t T = std::min((uint32_t)PF_CHUNK, n - c0);
+      if ((rc = pf_chunk(c, tokens + c0, T, pos + c0))) return rc;
+      last = T - 1;
+      if (c0 + T < n) HIPCHK(c, hipStreamSynchronize(c->stream));  // h_tokens is reused
+    }
+    const auto& cf = c->cfg;
+    HIPCHK(c, hipMemcpyAsync(c->x, c->pf_x + (size_t)last * cf.n_embd, (size_t)cf.n_embd * 4,
+                             hipMemcpyDeviceToDevice, c->stream));
+    const DevWeight* wout;
+    const float* onorm;
+    if ((rc = need_norm(c, "output_norm.weight", cf.n_embd, &onorm)) ||
+        (rc = need_matrix(c, "output.weight", cf.vocab_size, cf.n_embd, &wout)))
+      return rc;
+    memset(c->h_io, 0, 64);
+    c->h_io[ST_POS] = (int32_t)(pos + n - 1);
+    c->h_io[ST_TOKEN] = (int32_t)tokens[n - 1];
+    HIPCHK(c, hipMemcpyAsync(c->io, c->h_io, 64, hipMemcpyHostToDevice, c->stream));
+    enq_output(c, wout, onorm);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, c->stream, c->logits, cf.vocab_size, c->io, c->tokens, 0);
+    HIPCHK(c, hipGetLastError());
+    if (logits)
+      HIPCHK(c, hipMemcpyAsync(c->h_out, c->logits, (size_t)cf.vocab_size * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->h_io, c->io, 64, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (logits) memcpy(logits, c->h_out, (size_t)cf.vocab_size * 4);
+    if (argmax) *argmax = (uint32_t)c->h_io[ST_ARGMAX];
+    return TALOS_OK;
+  }
   for (uint32_t i = 0; i < n; ++i) c->h_tokens[i] = (int32_t)tokens[i];
   HIPCHK(c, hipMemcpyAsync(c->tokens, c->h_tokens, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
   memset(c->h_io, 0, 64);

@@ -2,8 +2,11 @@
 
 The reference fills its cache with one Model::step per prompt token
 (src/main.rs:88-94).  talos_hip_prefill runs that loop with the tokens fed
-on the device.  It must equal a host loop of forward_token bit for bit
-(logits and cache), and the oracle within the quantized tolerance.
+on the device (TALOS_HIP_BATCH=0, and any shape the batched kernels do not
+take), which must equal a host loop of forward_token bit for bit (logits and
+cache); by default it processes the prompt in batches on the matrix cores,
+which must agree with that loop and with the oracle within the quantized
+tolerance.
 
 Long context (7B shape, every matrix Q8_0, cache 16384 + 64 positions): the
 oracle cannot fill 16384 positions in test time, because its attention is a
@@ -41,9 +44,10 @@ def gqa(talos, oracle):
     m.close()
 
 
-def test_prefill_equals_token_loop(gqa, oracle):
-    """Device-fed prompt == host loop of forward_token, bit for bit, and the
-    oracle's prompt loop within 1e-3; the first greedy token agrees."""
+def test_prefill_equals_token_loop(gqa, talos, oracle, monkeypatch):
+    """Device-fed prompt (one step per token) == host loop of forward_token,
+    bit for bit; the batched prefill and the oracle's prompt loop within
+    1e-3 of it; the first greedy token agrees."""
     wl, m, ref = gqa
     prompt = _prompt(wl.spec.seed + 7, wl.prompt_len, wl.spec.vocab_size)
     n = len(prompt)
@@ -53,14 +57,23 @@ def test_prefill_equals_token_loop(gqa, oracle):
     for p, t in enumerate(prompt):
         host, am_host = m.forward_token(int(t), p)
     k_host, v_host = m.kv_read(n)
-    _step("gqa_q8 device prefill of the same prompt")
-    m.reset()
-    dev, am_dev = m.prefill(prompt, 0)
-    k_dev, v_dev = m.kv_read(n)
+    _step("gqa_q8 device token-by-token prefill of the same prompt")
+    monkeypatch.setenv("TALOS_HIP_BATCH", "0")
+    m1 = talos.Model.synth(wl.spec)
+    dev, am_dev = m1.prefill(prompt, 0)
+    k_dev, v_dev = m1.kv_read(n)
+    m1.close()
     assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))
     assert am_dev == am_host == oracle.argmax(dev)
     assert np.array_equal(k_dev.view(np.uint32), k_host.view(np.uint32))
     assert np.array_equal(v_dev.view(np.uint32), v_host.view(np.uint32))
+    _step("gqa_q8 batched prefill of the same prompt")
+    m.reset()
+    bat, am_bat = m.prefill(prompt, 0)
+    k_bat, v_bat = m.kv_read(n)
+    db = float(max(np.abs(bat - host).max(), np.abs(k_bat - k_host).max(), np.abs(v_bat - v_host).max()))
+    print(f"  batched vs token loop max-abs {db:.3e}", flush=True)
+    assert db <= TOL_Q and am_bat == am_host
     _step("gqa_q8 prefill vs the oracle's prompt loop")
     ref.reset()
     for p, t in enumerate(prompt):
