@@ -54,11 +54,13 @@ __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 #define TALOS_SPIN_LIMIT (1u << 20)
 
 struct GridSync {
-  uint32_t* flags;  // [nblocks * 16]: one 64-byte line per block
-  uint32_t* go;     // release word written by block 0
-  uint32_t* err;    // set to 1 when a wait timed out
+  uint32_t* flags;   // [nblocks * 16]: one 64-byte line per block
+  uint32_t* go;      // release word written by block 0
+  uint32_t* err;     // set to 1 when a wait timed out
+  uint32_t* packed;  // [nblocks rounded up to 4], 8-byte aligned: the same arrivals, one word per block
   uint32_t nblocks;
-  uint32_t spin;    // polls before a wait gives up
+  uint32_t spin;     // polls before a wait gives up
+  int one_hop;       // grid_wait: every block reads the packed arrivals itself
 };
 
 // Shared flag: a wait timed out before this barrier, so it is skipped.
@@ -80,13 +82,41 @@ __device__ __forceinline__ void grid_arrive(const GridSync& g, uint32_t ep) {
   if (threadIdx.x == 0) {
     barrier_skip() = ld_coh_u(g.err);
     st_coh_u(g.flags + blockIdx.x * 16, ep);
+    st_coh_u(g.packed + blockIdx.x, ep);
   }
+}
+
+// Arrival words b0 .. b0 + 3 of the packed array have reached ep (words at
+// or beyond nblocks count as reached).
+__device__ __forceinline__ bool packed_reached(const GridSync& g, uint32_t b0, uint32_t ep) {
+  const uint64_t* p = reinterpret_cast<const uint64_t*>(g.packed + b0);
+  const uint64_t a = __hip_atomic_load(gptr(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t c = __hip_atomic_load(gptr(p + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t w[4] = {(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)c, (uint32_t)(c >> 32)};
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ok &= b0 + i >= g.nblocks || (int32_t)(w[i] - ep) >= 0;
+  return ok;
 }
 
 __device__ __forceinline__ void grid_wait(const GridSync& g, uint32_t ep) {
   __syncthreads();
   const bool skip = barrier_skip() != 0;
-  if (blockIdx.x == 0) {
+  if (g.one_hop) {
+    // wave 0 reads all arrivals, four words per lane per pass
+    if (threadIdx.x < 64 && !skip) {
+      uint32_t s = 0;
+      for (;;) {
+        bool ok = true;
+        for (uint32_t b0 = threadIdx.x * 4; b0 < g.nblocks; b0 += 256) ok &= packed_reached(g, b0, ep);
+        if (__all(ok)) break;
+        if (++s > g.spin) {
+          if (threadIdx.x == 0) st_coh_u(g.err, 1u);
+          break;
+        }
+      }
+    }
+  } else if (blockIdx.x == 0) {
     if (!skip) {
       for (uint32_t w = threadIdx.x; w < g.nblocks; w += blockDim.x) {
         uint32_t s = 0;

@@ -113,9 +113,8 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
     r0 = p * R;
     rmax = A0.rows;
   };
-  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
-    pf();
-    stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
+  auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
+    stage_x_then(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     if (lane != 0) return;
@@ -176,10 +175,9 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
     r0 = (ubase + k) * R;
     rmax = P.m.rows;
   };
-  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
-    pf();
-    stage_x(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
-            P.need & 2);
+  auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
+    stage_x_then(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
+                 P.need & 2, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     const uint32_t r0 = (ubase + k) * R;
@@ -225,9 +223,8 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
     r0 = (ubase + k) * PR;
     rmax = P.g.rows;
   };
-  auto stage = [&](auto&& pf) {  // weight loads first: the input is a previous kernel's output
-    pf();
-    stage_x(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2);
+  auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
+    stage_x_then(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     const uint32_t p0 = (ubase + k) * PR;

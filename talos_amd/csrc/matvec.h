@@ -165,3 +165,87 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int n, cons
   }
   __syncthreads();
 }
+
+// stage_x with every load of x (and w) issued in one batch, B float4 per
+// thread (n % 4 == 0, n <= B * 1024), and `after()` run right behind that
+// batch: a wave's loads return in issue order, so weight loads issued there
+// do not delay x.  Same operations in the same order as stage_x, so the
+// same bits.
+template <int B, class After>
+__device__ __forceinline__ void stage_x_batch(const float* __restrict__ x, int n, const float* __restrict__ w,
+                                              float eps, bool norm, float* xs0, float* xs1, float* xsum,
+                                              float* red, bool need0, bool need1, After after) {
+  const int tid = threadIdx.x;
+  const int nr = n >> 2, n4 = ((n + 15) & ~15) >> 2;
+  f4 v[B], wv[B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    const int e4 = i * 256 + tid;
+    v[i] = *reinterpret_cast<const f4*>(x + (size_t)(e4 < nr ? e4 : nr - 1) * 4);
+  }
+  if (norm) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int e4 = i * 256 + tid;
+      wv[i] = *reinterpret_cast<const f4*>(w + (size_t)(e4 < nr ? e4 : nr - 1) * 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  after();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < B; ++i)
+    if (i * 256 + tid >= nr) v[i] = f4{0.f, 0.f, 0.f, 0.f};
+  float scale = 1.f;
+  if (norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < B; ++i)
+      if (i * 256 + tid < n4) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    ss = block_sum(ss, red, 4);
+    scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    const int e4 = i * 256 + tid;
+    if (i * 256 >= n4) break;  // uniform: no thread of this round holds a group
+    f4 vv = v[i];
+    if (e4 < n4) {
+      if (norm) {
+        const f4 ww = e4 < nr ? wv[i] : f4{0.f, 0.f, 0.f, 0.f};
+        vv.x = vv.x * scale * ww.x;
+        vv.y = vv.y * scale * ww.y;
+        vv.z = vv.z * scale * ww.z;
+        vv.w = vv.w * scale * ww.w;
+      }
+      if (need0) *reinterpret_cast<f4*>(xs0 + xidx<0>(e4 * 4)) = vv;
+      if (need1) *reinterpret_cast<f4*>(xs1 + xidx<1>(e4 * 4)) = vv;
+    }
+    float s = (vv.x + vv.y) + (vv.z + vv.w);
+    s = quad_sum(s);
+    if (e4 < n4 && (tid & 3) == 0) xsum[e4 >> 2] = s;
+  }
+  __syncthreads();
+}
+
+// Stage x for a matvec kernel whose first weight loads `after()` issues:
+// one batch of x loads ahead of them when n allows, else after them.
+template <class After>
+__device__ __forceinline__ void stage_x_then(const float* __restrict__ x, int n, const float* __restrict__ w,
+                                             float eps, bool norm, float* xs0, float* xs1, float* xsum,
+                                             float* red, bool need0, bool need1, After after) {
+  const int n4 = ((n + 15) & ~15) >> 2;
+  if (n & 3) {
+    after();
+    stage_x(x, n, w, eps, norm, xs0, xs1, xsum, red, need0, need1);
+  } else if (n4 <= 256) {
+    stage_x_batch<1>(x, n, w, eps, norm, xs0, xs1, xsum, red, need0, need1, after);
+  } else if (n4 <= 512) {
+    stage_x_batch<2>(x, n, w, eps, norm, xs0, xs1, xsum, red, need0, need1, after);
+  } else if (n4 <= 1024) {
+    stage_x_batch<4>(x, n, w, eps, norm, xs0, xs1, xsum, red, need0, need1, after);
+  } else {
+    after();
+    stage_x(x, n, w, eps, norm, xs0, xs1, xsum, red, need0, need1);
+  }
+}

@@ -51,7 +51,7 @@ struct MegaParams {
   uint32_t* count;
   int32_t* state;
   int32_t* tokens;
-  uint32_t* sync;  // [nblocks*16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64]
+  uint32_t* sync;  // mega_sync_words(nblocks) words, laid out as that function describes
   uint32_t nsplit, max_chunk;
   int attn_direct;  // sequences up to this length: one attention item per q head
   int attn_wait;    // attention blocks wait for their q/k/v producers only, not a grid barrier
@@ -63,6 +63,7 @@ struct MegaParams {
   int prefetch;  // issue each matvec phase's first weight loads before its barrier wait
   uint64_t* timeline;  // optional: [nblocks][MEGA_TL_SLOTS] wall-clock marks
   uint32_t spin_limit; // polls before a bounded wait gives up (then ST_ERR is set)
+  int one_hop;         // grid barriers: every block reads all arrivals (no release word)
 };
 
 // Read-only tables read through the constant address space compile to
@@ -125,7 +126,11 @@ __device__ __forceinline__ float* mega_base(const MegaParams& P, uint32_t l) {
       (P).timeline[(size_t)blockIdx.x * MEGA_TL_SLOTS((P).n_layer) + (slot)] = wall_clock64(); \
   } while (0)
 
-static inline size_t mega_sync_words(uint32_t nblocks) { return (size_t)nblocks * 16 + 64 + 2 * nblocks + 64; }
+// [nblocks * 16 flags][go @+0][epoch base @+16][done @+32][argmax pairs @+64,
+// 2 * nblocks words][packed arrivals, nblocks words rounded up to 4]
+static inline size_t mega_sync_words(uint32_t nblocks) {
+  return (size_t)nblocks * 16 + 64 + 2 * nblocks + ((nblocks + 3) & ~3u) + 64;
+}
 
 // Stage n floats into the LDS layouts, optionally as rmsnorm(x)*w
 // (src/math/ops.rs:5-12), with every load of the block (x and the norm
@@ -704,6 +709,8 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
   G.err = reinterpret_cast<uint32_t*>(P.state + ST_ERR);
   G.nblocks = nb;
   G.spin = P.spin_limit;
+  G.packed = P.sync + nb * 16 + 64 + 2 * nb;
+  G.one_hop = P.one_hop;
   uint32_t* epoch_p = P.sync + nb * 16 + 16;
   uint32_t* done = P.sync + nb * 16 + 32;
   int32_t* amx = reinterpret_cast<int32_t*>(P.sync + nb * 16 + 64);

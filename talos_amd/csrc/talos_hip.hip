@@ -151,6 +151,7 @@ struct talos_hip_ctx {
   float* mact = nullptr;   // per-layer activation slots
   float* mpart = nullptr;  // per-layer attention slice partials
   bool mega_prefetch = true;  // TALOS_HIP_PREFETCH=0 turns cross-barrier weight prefetch off
+  bool one_hop = true;        // TALOS_HIP_BAR1=0: grid barriers through block 0's release word
   // The persistent kernel goes out as an ordinary launch: its grid is one
   // workgroup per CU and the set-up's occupancy check admits it only when at
   // least one fits per CU, so on an otherwise idle device every workgroup is resident
@@ -847,6 +848,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.part = c->mpart;
   P.pstride = pstride;
   P.prefetch = c->mega_prefetch ? 1 : 0;
+  P.one_hop = c->one_hop ? 1 : 0;
   P.count = c->count;
   P.state = c->io;
   P.tokens = c->tokens;
@@ -1122,6 +1124,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_mega = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_PREFETCH");
   c->mega_prefetch = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_BAR1");
+  c->one_hop = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_COOP");
   c->mega_coop = env && env[0] == '1';
   env = getenv("TALOS_HIP_MFMA");
@@ -1631,6 +1635,19 @@ static int enqueue_matvec(talos_hip_ctx* c, const DevWeight* w, const float* d_x
   const size_t lds = stage_lds_bytes((int)w->cols, R.need);
   if (lds > c->max_lds) return fail(c, TALOS_ERR_SHAPE, "cols %zu needs %zu B of LDS", w->cols, lds);
   uint32_t blocks;
+  if (w->mat.fmt == TALOS_FMT_F32) {
+    // two rows per wave: twice the waves of mv_rows(F32) = 4, more bytes in
+    // flight per CU (a standalone F32 matvec of 4096 x 4096 streams at ~0.68
+    // of peak this way, ~0.56 with four rows)
+    R.units = (uint32_t)((w->rows + 1) / 2);
+    plan(R.units, R.upw, blocks);
+    const int u = mv_u(w->mat.nchunk);
+    if (u >= 4) hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 4>), dim3(blocks), dim3(256), lds, c->stream, R);
+    else if (u == 2) hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 2>), dim3(blocks), dim3(256), lds, c->stream, R);
+    else hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 1>), dim3(blocks), dim3(256), lds, c->stream, R);
+    HIPCHK(c, hipGetLastError());
+    return TALOS_OK;
+  }
   plan(R.units, R.upw, blocks);
   TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), lds, c->stream, R);
   HIPCHK(c, hipGetLastError());

@@ -71,6 +71,7 @@ def test_tiny_f32_parity_and_greedy(tiny):
     prompt = _prompt(wl.spec.seed + 1, wl.prompt_len, wl.spec.vocab_size)
     logits, gen = _parity(m, ref, prompt, wl.decode_steps, 1e-4)
     assert len(gen) == wl.decode_steps
+    record_parity("tiny_f32_8+64", _parity.worst, 1e-4, steps=wl.prompt_len + wl.decode_steps, path=m.path())
     # Determinism (tests/forward_gpu.rs:183-190): rerun, bit-identical logits.
     _step("tiny_f32 rerun determinism")
     m.reset()
@@ -235,6 +236,7 @@ def test_mistral7b_q4_short_parity(talos, oracle):
     prompt = _prompt(wl.spec.seed + 1, 4, wl.spec.vocab_size)
     _step("mistral7b_q4 parity 4 + 4")
     _parity(m, ref, prompt, 4, 1e-3)
+    record_parity("mistral7b_q4_4+4_ctx256", _parity.worst, 1e-3, steps=8, path=m.path())
     ref.close()
     m.close()
 
@@ -252,6 +254,7 @@ def test_mistral7b_q4_matrix_core_parity(talos, oracle, monkeypatch):
     prompt = _prompt(wl.spec.seed + 2, 4, wl.spec.vocab_size)
     _step("mistral7b_q4 matrix-core parity 4 + 4")
     _parity(m, ref, prompt, 4, 1e-3)
+    record_parity("mistral7b_q4_4+4_matrix_cores", _parity.worst, 1e-3, steps=8, path=m.path())
     ref.close()
     m.close()
 
@@ -269,5 +272,7 @@ def test_gqa_q8_f32_x_parity(talos, oracle, monkeypatch):
     ref = oracle.OracleModel(m.gguf_view(), nthreads=8)
     prompt = _prompt(wl.spec.seed + 3, wl.prompt_len, wl.spec.vocab_size)
     _parity(m, ref, prompt, 32, 1e-3)
+    record_parity("gqa_q8_16+32_f32_x_split_attention", _parity.worst, 1e-3, steps=wl.prompt_len + 32,
+                  path=m.path())
     ref.close()
     m.close()

@@ -20,6 +20,8 @@ cache must read back exactly what was written.
 import numpy as np
 import pytest
 
+from tests.conftest import record_parity
+
 pytestmark = pytest.mark.gpu
 
 TOL_Q = 1e-3  # quantized formats: max-abs on logits
@@ -144,12 +146,15 @@ def test_long_q8_short_prompt_parity(long_q8, oracle):
     g, tok = m.prefill(prompt, 0)
     for p, t in enumerate(prompt):
         c = ref.forward(int(t), p)
+    worst = 0.0
     for s in range(5):
         d = float(np.abs(g - c).max())
+        worst = max(worst, d)
         print(f"  pos {len(prompt) - 1 + s}: max-abs logit diff {d:.3e}", flush=True)
         assert d <= TOL_Q
         assert tok == oracle.argmax(c)
         if s == 4:
+            record_parity("mistral7b_q8_4+4_batched_prefill", worst, TOL_Q, steps=8, path=m.path())
             break
         pos = len(prompt) + s
         g, nxt = m.forward_token(tok, pos)
@@ -197,6 +202,7 @@ def test_long_context_decode_parity(long_q8, oracle):
         greedy.append(ga)
         tok = ga
     print(f"  worst {worst:.3e}", flush=True)
+    record_parity("mistral7b_q8_16k_seeded_kv_3_steps", worst, TOL_Q, steps=3, path=m.path())
     # The device greedy loop over the 64 steps of the workload, twice:
     # bit-identical reruns, and its first steps are the oracle's greedy tokens.
     _step(f"decode_greedy {wl.decode_steps} steps from pos {P}, twice")

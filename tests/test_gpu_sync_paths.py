@@ -9,7 +9,9 @@ At the 7B shape (Q4_0 layers, Q6_K output) the default decode step
   * runs the down-projection's column quarters on different workgroups, the
     quarter sums added in quarter order by the next staging.
 TALOS_HIP_ATTN_WAIT=0 puts full grid barriers back (and the gate/up pairs
-strided over the waves); TALOS_HIP_DSPLIT=1
+strided over the waves); TALOS_HIP_BAR1=0 makes every grid barrier wait for
+block 0's release word instead of reading all arrivals itself;
+TALOS_HIP_DSPLIT=1
 splits the quarters over the waves of one workgroup, summed in the same
 order in LDS.  Neither changes an arithmetic operation or its order, so the
 logits and the cache must match the default bit for bit (the default path
@@ -35,15 +37,23 @@ def _run(talos, spec, prompt):
         m.close()
 
 
-def test_sync_variants_bit_identical(talos, monkeypatch):
+@pytest.mark.parametrize("direct", [None, "0"], ids=["attn_default", "attn_split"])
+def test_sync_variants_bit_identical(talos, monkeypatch, direct):
+    """With TALOS_HIP_ATTN_DIRECT=0 in both runs the attention takes its
+    split-sequence items at every length, so the producer-only waits of the
+    attention slices run together with the gate/up runs and the quarter
+    down waits and are compared against full barriers too."""
     from talos_amd import configs
     wl = configs.mistral7b_q4(ctx=256)
     prompt = np.random.default_rng(wl.spec.seed + 11).integers(0, wl.spec.vocab_size, 6).astype(np.uint32)
-    print("\n[sync] default synchronisation", flush=True)
+    if direct is not None:
+        monkeypatch.setenv("TALOS_HIP_ATTN_DIRECT", direct)
+    print(f"\n[sync] default synchronisation (attention direct={direct})", flush=True)
     base, kb, vb = _run(talos, wl.spec, prompt)
     monkeypatch.setenv("TALOS_HIP_ATTN_WAIT", "0")
     monkeypatch.setenv("TALOS_HIP_DSPLIT", "1")
-    print("[sync] grid barriers, in-workgroup quarter split", flush=True)
+    monkeypatch.setenv("TALOS_HIP_BAR1", "0")
+    print("[sync] two-hop grid barriers, in-workgroup quarter split", flush=True)
     alt, ka, va = _run(talos, wl.spec, prompt)
     for i, ((a, am_a), (b, am_b)) in enumerate(zip(base, alt)):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"pos {i}: logits differ"
