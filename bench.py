@@ -106,7 +106,12 @@ def phase_breakdown(tl, n_layer: int, per_layer: int = 20, bar: int = 16) -> dic
 def matvec_microbench(T) -> dict:
     """W[4096 x 4096] . x[4096] in F32, Q8_0 and Q4_0 (W ~ N(0, 0.02)),
     rotating over enough resident copies (> 256 MB) that every launch
-    streams W from HBM.  GB/s of algorithmic bytes (W + x + y)."""
+    streams W from HBM.  GB/s of algorithmic bytes (W + x + y) per launch,
+    launched back to back on one stream.  `copy_us` is a plain device copy
+    of the matrix's size launched the same way: one launch of a kernel that
+    reads those bytes (and writes as many) costs at least that, so
+    `copy_frac` (the matvec's bytes over copy_us, against peak) is what a
+    single-launch matvec of this size can reach."""
     n = 4096
     be = T.HipBackend(1, 32, 8, n, n, 32, 16)
     w = T.synth_normal(7, "matvec.W", 0, n * n, 0.02)
@@ -118,8 +123,10 @@ def matvec_microbench(T) -> dict:
         for nm in names:
             be.upload(nm, data, t, n, n)
         us, b = be.bench_matvec(names, 256)
+        cus = be.bench_copy((data.nbytes + 15) // 16 * 16, 256)
         res[name] = {"us": round(us, 2), "GB/s": round(b / (us * 1e-6) / 1e9, 1),
-                     "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b)}
+                     "frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b),
+                     "copy_us": round(cus, 2), "copy_frac": round(b / (cus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     be.close()
     log(f"matvec 4096x4096: {res}")
     return res

@@ -251,6 +251,14 @@ class HipBackend:
         self._check(lib().talos_hip_bench_matvec(self._h, arr, len(names), reps, C.byref(us), C.byref(b)))
         return us.value, b.value
 
+    def bench_copy(self, nbytes: int, reps: int) -> float:
+        """Mean microseconds of a plain device copy of nbytes (read + write),
+        back to back on this context's stream: the launch floor beside
+        bench_matvec."""
+        us = C.c_float()
+        self._check(lib().talos_hip_bench_copy(self._h, nbytes, reps, C.byref(us)))
+        return us.value
+
     def sample_dev(self, d_logits: int, n: int, d_token: int, temperature: float, top_k=None, top_p=None,
                    u: float = 0.5):
         """talos_hip_sample_dev on device pointers (enqueued, not waited for)."""

@@ -30,6 +30,7 @@
 #include "mega_inst.h"
 #include "sample.h"
 #include "prefill.h"
+#include "rows_iq.h"
 
 // Scratch of the allocation-free sampling entry point
 // (talos_hip_sample_noalloc): keys twice and the probabilities for up to
@@ -1645,6 +1646,34 @@ static int enqueue_matvec(talos_hip_ctx* c, const DevWeight* w, const float* d_x
     if (u >= 4) hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 4>), dim3(blocks), dim3(256), lds, c->stream, R);
     else if (u == 2) hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 2>), dim3(blocks), dim3(256), lds, c->stream, R);
     else hipLaunchKernelGGL((k_rows<TALOS_FMT_F32, 2, 1>), dim3(blocks), dim3(256), lds, c->stream, R);
+    HIPCHK(c, hipGetLastError());
+    return TALOS_OK;
+  }
+  const int nr = rows_iq_rounds(w->cols);
+  if ((w->mat.fmt == TALOS_FMT_Q4_0 || w->mat.fmt == TALOS_FMT_Q8_0) && nr && c->allow_dot4) {
+    plan(R.units, R.upw, blocks);
+    const size_t lq = rows_iq_lds_bytes(w->cols);
+    const int u = mv_u(w->mat.nchunk);
+#define IQ_NR(F, U_)                                                                                       \
+  do {                                                                                                     \
+    constexpr int RR = mv_rows(F);                                                                         \
+    switch (nr) {                                                                                          \
+      case 1: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 1>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
+      case 2: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 2>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
+      case 4: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 4>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
+      default: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 8>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
+    }                                                                                                      \
+  } while (0)
+#define IQ_U(F)                   \
+  do {                            \
+    if (u >= 4) IQ_NR(F, 4);      \
+    else if (u == 2) IQ_NR(F, 2); \
+    else IQ_NR(F, 1);             \
+  } while (0)
+    if (w->mat.fmt == TALOS_FMT_Q4_0) IQ_U(TALOS_FMT_Q4_0);
+    else IQ_U(TALOS_FMT_Q8_0);
+#undef IQ_U
+#undef IQ_NR
     HIPCHK(c, hipGetLastError());
     return TALOS_OK;
   }
