@@ -103,13 +103,19 @@ __device__ __forceinline__ void grid_wait(const GridSync& g, uint32_t ep) {
   __syncthreads();
   const bool skip = barrier_skip() != 0;
   if (g.one_hop) {
-    // wave 0 reads all arrivals, four words per lane per pass
+    // wave 0 reads all arrivals, four words per lane per pass (nblocks <=
+    // 8192); a lane stops reading words that have arrived, so a long wait
+    // ends up polling only the stragglers' words
     if (threadIdx.x < 64 && !skip) {
+      uint32_t pending = 0;  // bit k: words 4 * lane + 256 k .. +3 not all arrived yet
+      for (uint32_t k = 0, b0 = threadIdx.x * 4; b0 < g.nblocks && k < 32; b0 += 256, ++k) pending |= 1u << k;
       uint32_t s = 0;
       for (;;) {
-        bool ok = true;
-        for (uint32_t b0 = threadIdx.x * 4; b0 < g.nblocks; b0 += 256) ok &= packed_reached(g, b0, ep);
-        if (__all(ok)) break;
+        for (uint32_t p = pending; p; p &= p - 1) {
+          const uint32_t k = __builtin_ctz(p);
+          if (packed_reached(g, threadIdx.x * 4 + 256 * k, ep)) pending &= ~(1u << k);
+        }
+        if (__all(pending == 0)) break;
         if (++s > g.spin) {
           if (threadIdx.x == 0) st_coh_u(g.err, 1u);
           break;

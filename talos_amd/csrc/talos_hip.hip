@@ -849,7 +849,7 @@ int mega_setup(talos_hip_ctx* c) {
   P.part = c->mpart;
   P.pstride = pstride;
   P.prefetch = c->mega_prefetch ? 1 : 0;
-  P.one_hop = c->one_hop ? 1 : 0;
+  P.one_hop = c->one_hop && c->mega_blocks <= 8192 ? 1 : 0;
   P.count = c->count;
   P.state = c->io;
   P.tokens = c->tokens;
