@@ -114,10 +114,18 @@ int talos_hip_forward_token(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, fl
 int talos_hip_decode_greedy(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, uint32_t n_steps,
                             uint32_t* tokens_out);
 
-/* Prompt feed on the device: run tokens[0..n) at positions pos..pos+n-1,
- * one forward each (the prefill loop of src/main.rs:88-94, Model::step per
- * prompt token), with each next token taken from a device copy of `tokens`
- * so the host only launches.  Returns the last step's logits (nullable) and
+/* Prompt processing on the device: run tokens[0..n) at positions
+ * pos..pos+n-1 (the prefill loop of src/main.rs:88-94, Model::step per
+ * prompt token) and leave the cache and the device state as that loop does.
+ * Models whose layer matrices are F32, Q4_0 or Q8_0 with head_dim a
+ * multiple of 16 up to 256 (n_head * head_dim == n_embd, groups up to 8)
+ * take the prompt in chunks of up to 1024 tokens through each layer at once
+ * on the matrix cores: the same products and f32 sums in another order, so
+ * within f32 rounding of the token loop rather than bit-identical.  Other
+ * models, or any model with TALOS_HIP_BATCH=0 in the environment when the
+ * context is created, run one forward per token with each next token taken
+ * from a device copy of `tokens` (bit-identical to a host loop of
+ * talos_hip_forward_token).  Returns the last step's logits (nullable) and
  * argmax (nullable), which is the first greedy token.  pos + n must be
  * <= context_length and every token < vocab_size. */
 int talos_hip_prefill(talos_hip_ctx* ctx, const uint32_t* tokens, uint32_t n, uint32_t pos, float* logits,

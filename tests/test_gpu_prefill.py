@@ -37,7 +37,7 @@ def test_batched_prefill_matches_oracle(talos, oracle, which, n, tol):
     dk = float(max(np.abs(kg - kc).max(), np.abs(vg - vc).max()))
     print(f"  K/V cache max abs {dk:.3e}", flush=True)
     assert dk <= tol
-    record_parity(f"{which}_batched_prefill_{n}", max(d, dk), tol)
+    record_parity(f"{which}_batched_prefill_{n}", max(d, dk), tol, path="batched_prefill")
     ref.close()
     m.close()
 
@@ -66,7 +66,7 @@ def test_multi_chunk_prefill_and_continuation(talos, oracle, monkeypatch):
     dk = float(max(np.abs(kg - kc).max(), np.abs(vg - vc).max()))
     print(f"  last logits max abs {d:.3e}, K/V max abs {dk:.3e}", flush=True)
     assert d <= 1e-3 and dk <= 1e-3 and am == oracle.argmax(c)
-    record_parity("gqa_q8_batched_prefill_2100", max(d, dk), 1e-3)
+    record_parity("gqa_q8_batched_prefill_2100", max(d, dk), 1e-3, path="batched_prefill")
     ref.close()
     m.close()
     _step("the same prompt one step per token")
