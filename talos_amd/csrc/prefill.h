@@ -45,100 +45,192 @@ __global__ __launch_bounds__(256) void k_pf_rmsnorm(const float* __restrict__ X,
 }
 
 // ------------------------------------------------------------- the GEMM --
-// Y[t][r] (+)= sum_k Xn[t][k] W[r][k] for t < T, r < M (Y's row pitch ldy).
-// Block: 4 waves, a tile of 64 tokens x 64 rows; wave w owns rows
-// [64 bx + 16 w, +16) for all 64 tokens (four 16 x 16 MFMA tiles).  Per
-// 64-wide K chunk the block stages Xn transposed in LDS, [k][token] with a
-// pitch of 80 floats (the 64 lanes of one A read hit 64 distinct banks);
-// each lane dequantizes its weight row's elements k = 4 s + l / 16 of every
-// 32-element block straight from the repacked layout.
+// Y_s[t][r] (+)= sum_k X[t][k] W_s[r][k] for t < T and the rows r of up to
+// three matrices W_s sharing X (q/k/v, gate/up: one launch).  Block: 8
+// waves, a tile of 64 tokens x 128 rows of one matrix; wave w owns rows
+// [128 tile + 16 w, +16) for all 64 tokens (four 16 x 16 MFMA tiles).  Per
+// 64-wide K chunk the block stages X transposed in LDS, [k][token] with a
+// pitch of 80 floats (the 64 lanes of one A read hit 64 distinct banks),
+// double buffered; each lane dequantizes its row's elements k = 4 s + l / 16
+// of every 32-element block straight from the repacked layout.  The next
+// chunk's weight and X loads are issued before the current chunk's MFMAs
+// (all unconditional, clamped addresses, so the wait counts stay exact).
+// Per output the products are summed in K order, chunk by chunk.
 #define PF_KC 64
 #define PF_AP 80
+#define PF_TOK 64
+#define PF_ROWS 128
+#define PF_NT 512
+
+struct PfSeg {
+  DevMat W;
+  float* Y;       // [T][ldy]
+  uint32_t ldy;
+  uint32_t tiles;  // ceil(W.rows / PF_ROWS)
+};
 
 struct PfGemm {
-  DevMat W;
-  const float* X;   // [T][K]
-  float* Y;         // [T][ldy]
-  uint32_t T, K, M, ldy;
+  PfSeg S[3];
+  uint32_t nseg;
+  const float* X;  // [T][K], K % 4 == 0
+  uint32_t T, K;
   int accumulate;
 };
 
+// One lane's weights of a 64-wide K chunk: two 32-element blocks of its row.
 template <uint32_t FMT>
-__global__ __launch_bounds__(256) void k_pf_gemm(PfGemm G) {
-  __shared__ float As[PF_KC * PF_AP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, li = lane & 15;
-  const uint32_t tb = blockIdx.y * 64;
-  const uint32_t row = blockIdx.x * 64 + wave * 16 + li;
-  const uint32_t rowc = row < G.M ? row : G.M - 1;
-  pf4 acc[4];
+struct PfW {
+  u4 q[2][FMT == TALOS_FMT_Q8_0 ? 2 : 1];
+  uint32_t d;  // the two blocks' f16 scales
+};
+template <>
+struct PfW<TALOS_FMT_F32> {
+  float v[2][8];
+};
+
+template <uint32_t FMT>
+__device__ __forceinline__ void pf_load_w(PfW<FMT>& F, const DevMat& W, uint32_t rowc, uint32_t k0, uint32_t K,
+                                          int g) {
+  if constexpr (FMT == TALOS_FMT_F32) {
+    const float* wr = reinterpret_cast<const float*>(W.q) + (size_t)rowc * W.nchunk * 4;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = pf4{0.f, 0.f, 0.f, 0.f};
-  for (uint32_t k0 = 0; k0 < G.K; k0 += PF_KC) {
-    // stage Xn[tb .. +64][k0 .. +64] transposed (zeros past T and K)
-    __syncthreads();
-    for (int i = tid; i < 64 * PF_KC; i += 256) {
-      const int tt = i / PF_KC, kk = i % PF_KC;
-      const uint32_t t = tb + tt, k = k0 + kk;
-      As[kk * PF_AP + tt] = (t < G.T && k < G.K) ? G.X[(size_t)t * G.K + k] : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int blk = 0; blk < PF_KC / 32; ++blk) {
-      const uint32_t kb = k0 + blk * 32;  // this 32-element block of K
-      float b[8];                         // W[row][kb + 4 s + g], s = 0..7
-      if constexpr (FMT == TALOS_FMT_Q4_0) {
-        const uint32_t nb = G.K / 32, bi = kb / 32 < nb ? kb / 32 : nb - 1;
-        const size_t ci = (size_t)rowc * nb + bi;
-        const u4 q = *reinterpret_cast<const u4*>(G.W.q + ci * 16);
-        const float d = f16_to_f32(G.W.d[ci]);
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-        // element e = 4 s + g: byte e & 15, low nibble for e < 16
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int e = 4 * s + g, by = e & 15;
-          const uint32_t v = (w4[by >> 2] >> (8 * (by & 3))) & 0xFFu;
-          const int nib = e < 16 ? (int)(v & 15u) : (int)(v >> 4);
-          b[s] = (kb < G.K) ? d * (float)(nib - 8) : 0.f;
-        }
-      } else if constexpr (FMT == TALOS_FMT_Q8_0) {
-        const uint32_t nb = G.K / 32, bi = kb / 32 < nb ? kb / 32 : nb - 1;
-        const size_t ci = (size_t)rowc * nb + bi;
-        const u4 q0 = *reinterpret_cast<const u4*>(G.W.q + ci * 32);
-        const u4 q1 = *reinterpret_cast<const u4*>(G.W.q + ci * 32 + 16);
-        const float d = f16_to_f32(G.W.d[ci]);
-        const uint32_t w8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int e = 4 * s + g;
-          const uint32_t v = ((w8[e >> 2] >> (8 * (e & 3))) & 0xFFu) ^ 0x80u;
-          b[s] = (kb < G.K) ? d * (float)(int8_t)v : 0.f;
-        }
-      } else {  // F32: rows padded to nchunk * 4 floats
-        const float* wr = reinterpret_cast<const float*>(G.W.q) + (size_t)rowc * G.W.nchunk * 4;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const uint32_t k = kb + 4 * s + g;
-          b[s] = k < G.K ? wr[k] : 0.f;
-        }
-      }
+    for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const int kk = blk * 32 + 4 * s + g;
+        const uint32_t k = k0 + 32 * blk + 4 * s + g;
+        F.v[blk][s] = wr[k < K ? k : K - 1];
+      }
+  } else {
+    const uint32_t nb = K / 32;
+    uint32_t dd[2];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[t] = mfma16x4(As[kk * PF_AP + 16 * t + li], b[s], acc[t]);
+    for (int blk = 0; blk < 2; ++blk) {
+      const uint32_t bi0 = (k0 + 32 * blk) / 32, bi = bi0 < nb ? bi0 : nb - 1;
+      const size_t ci = (size_t)rowc * nb + bi;
+      if constexpr (FMT == TALOS_FMT_Q4_0) {
+        F.q[blk][0] = *reinterpret_cast<const u4*>(W.q + ci * 16);
+      } else {
+        F.q[blk][0] = *reinterpret_cast<const u4*>(W.q + ci * 32);
+        F.q[blk][1] = *reinterpret_cast<const u4*>(W.q + ci * 32 + 16);
+      }
+      dd[blk] = W.d[ci];
+    }
+    F.d = dd[0] | (dd[1] << 16);
+  }
+}
+
+// b[s] = W[row][kb + 4 s + g] for block blk of the chunk (kb = its first
+// element; zero past K).
+template <uint32_t FMT>
+__device__ __forceinline__ void pf_dequant(const PfW<FMT>& F, int blk, uint32_t kb, uint32_t K, int g,
+                                           float (&b)[8]) {
+  if constexpr (FMT == TALOS_FMT_F32) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) b[s] = kb + 4 * s + g < K ? F.v[blk][s] : 0.f;
+  } else {
+    const float d = f16_to_f32((uint16_t)(F.d >> (16 * blk)));
+    if constexpr (FMT == TALOS_FMT_Q4_0) {
+      const uint32_t w4[4] = {F.q[blk][0].x, F.q[blk][0].y, F.q[blk][0].z, F.q[blk][0].w};
+      // element e = 4 s + g: byte e & 15, low nibble for e < 16
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int e = 4 * s + g, by = e & 15;
+        const uint32_t v = (w4[by >> 2] >> (8 * (by & 3))) & 0xFFu;
+        const int nib = e < 16 ? (int)(v & 15u) : (int)(v >> 4);
+        b[s] = kb < K ? d * (float)(nib - 8) : 0.f;
+      }
+    } else {
+      const uint32_t w8[8] = {F.q[blk][0].x, F.q[blk][0].y, F.q[blk][0].z, F.q[blk][0].w,
+                              F.q[blk][1].x, F.q[blk][1].y, F.q[blk][1].z, F.q[blk][1].w};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int e = 4 * s + g;
+        const uint32_t v = ((w8[e >> 2] >> (8 * (e & 3))) & 0xFFu) ^ 0x80u;
+        b[s] = kb < K ? d * (float)(int8_t)v : 0.f;
       }
     }
   }
+}
+
+// X[tb .. +64][k0 .. +64]: float4 e = tid + 512 j holds token e % 64,
+// elements k0 + 4 (e / 64) .. +3 (zero past T and K).
+struct PfX {
+  f4 v[2];
+};
+__device__ __forceinline__ void pf_load_x(PfX& P, const float* __restrict__ X, uint32_t T, uint32_t K, uint32_t tb,
+                                          uint32_t k0, int tid) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid + PF_NT * j;
+    const uint32_t t = tb + (uint32_t)(e & 63), k = k0 + 4u * (uint32_t)(e >> 6);
+    const uint32_t tc = t < T ? t : T - 1, kc = k < K ? k : K - 4;
+    const f4 x = *reinterpret_cast<const f4*>(X + (size_t)tc * K + kc);
+    P.v[j] = (t < T && k < K) ? x : f4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+__device__ __forceinline__ void pf_store_x(const PfX& P, float* As, int tid) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = tid + PF_NT * j, tt = e & 63, k4 = e >> 6;
+    As[(4 * k4 + 0) * PF_AP + tt] = P.v[j].x;
+    As[(4 * k4 + 1) * PF_AP + tt] = P.v[j].y;
+    As[(4 * k4 + 2) * PF_AP + tt] = P.v[j].z;
+    As[(4 * k4 + 3) * PF_AP + tt] = P.v[j].w;
+  }
+}
+
+template <uint32_t FMT>
+__global__ __launch_bounds__(PF_NT) void k_pf_gemm(PfGemm G) {
+  __shared__ float As[2][PF_KC * PF_AP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  // this block's matrix and row tile
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
+  const PfSeg& S = G.S[s];
+  const uint32_t M = S.W.rows;
+  const uint32_t tb = blockIdx.y * PF_TOK;
+  const uint32_t row = tile * PF_ROWS + (uint32_t)wave * 16 + li;
+  const uint32_t rowc = row < M ? row : M - 1;
+  pf4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = pf4{0.f, 0.f, 0.f, 0.f};
+  const int nchunks = (int)((G.K + PF_KC - 1) / PF_KC);
+  PfW<FMT> wc, wn;
+  PfX xc, xn;
+  pf_load_w<FMT>(wc, S.W, rowc, 0, G.K, g);
+  pf_load_x(xc, G.X, G.T, G.K, tb, 0, tid);
+  for (int c = 0; c < nchunks; ++c) {
+    float* A = As[c & 1];
+    pf_store_x(xc, A, tid);
+    __syncthreads();
+    // the next chunk's loads (the last chunk again when there is none)
+    const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
+    pf_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
+    pf_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      float b[8];
+      pf_dequant<FMT>(wc, blk, k0 + 32 * blk, G.K, g, b);
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) {
+        const int kk = blk * 32 + 4 * s8 + g;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16x4(A[kk * PF_AP + 16 * t + li], b[s8], acc[t]);
+      }
+    }
+    wc = wn;
+    xc = xn;
+  }
   // D[4 g + r][li] of tile t: token tb + 16 t + 4 g + r, weight row `row`
-  if (row < G.M) {
+  if (row < M) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t tok = tb + 16 * t + 4 * g + r;
         if (tok < G.T) {
-          float* y = G.Y + (size_t)tok * G.ldy + row;
+          float* y = S.Y + (size_t)tok * S.ldy + row;
           *y = G.accumulate ? *y + acc[t][r] : acc[t][r];
         }
       }

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -962,7 +963,8 @@ void enq_sample(talos_hip_ctx* c, const float* logits, uint32_t n, float tempera
 // with groups of at most 8.
 int pf_supported(talos_hip_ctx* c, bool* ok) {
   *ok = false;
-  if (!c->allow_batch || c->hd % 16 || c->hd > 256 || c->group > 8 || c->cfg.n_embd != c->cfg.n_head * c->hd)
+  if (!c->allow_batch || c->hd % 16 || c->hd > 256 || c->group > 8 || c->cfg.n_embd != c->cfg.n_head * c->hd ||
+      c->cfg.n_ff % 4)
     return TALOS_OK;
   for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
     LayerW w;
@@ -996,22 +998,39 @@ int pf_reserve(talos_hip_ctx* c, uint32_t T) {
   return TALOS_OK;
 }
 
-// Y[T][ldy] (+)= X[T][w.cols] W^T
-void enq_gemm(talos_hip_ctx* c, const DevWeight* w, const float* X, uint32_t T, float* Y, uint32_t ldy, int acc) {
-  PfGemm G{};
-  G.W = w->mat;
-  G.X = X;
-  G.Y = Y;
-  G.T = T;
-  G.K = (uint32_t)w->cols;
-  G.M = (uint32_t)w->rows;
-  G.ldy = ldy;
-  G.accumulate = acc;
-  const dim3 grid((G.M + 63) / 64, (T + 63) / 64);
-  switch (w->type) {
-    case TALOS_GGML_Q4_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(256), 0, c->stream, G); break;
-    case TALOS_GGML_Q8_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(256), 0, c->stream, G); break;
-    default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(256), 0, c->stream, G); break;
+// Y_i[T][ldy_i] (+)= X[T][K] W_i^T for matrices sharing X; consecutive ones
+// of one format go out as one launch (up to three).
+struct GemmOut {
+  const DevWeight* w;
+  float* y;
+  uint32_t ldy;
+};
+void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float* X, uint32_t T, int acc) {
+  const GemmOut* o = outs.begin();
+  const size_t n = outs.size();
+  for (size_t i = 0; i < n;) {
+    PfGemm G{};
+    G.X = X;
+    G.T = T;
+    G.K = (uint32_t)o[i].w->cols;
+    G.accumulate = acc;
+    const uint32_t type = o[i].w->type;
+    uint32_t tiles = 0;
+    while (i < n && G.nseg < 3 && o[i].w->type == type) {
+      PfSeg& S = G.S[G.nseg++];
+      S.W = o[i].w->mat;
+      S.Y = o[i].y;
+      S.ldy = o[i].ldy;
+      S.tiles = (uint32_t)((o[i].w->rows + PF_ROWS - 1) / PF_ROWS);
+      tiles += S.tiles;
+      ++i;
+    }
+    const dim3 grid(tiles, (T + PF_TOK - 1) / PF_TOK);
+    switch (type) {
+      case TALOS_GGML_Q4_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G); break;
+      case TALOS_GGML_Q8_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G); break;
+      default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(PF_NT), 0, c->stream, G); break;
+    }
   }
 }
 
@@ -1064,20 +1083,17 @@ int pf_chunk(talos_hip_ctx* c, const uint32_t* tokens, uint32_t T, uint32_t p0) 
     LayerW w;
     if ((rc = layer_weights(c, l, &w))) return rc;
     hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.an, cf.rms_eps, n, c->pf_xn);
-    enq_gemm(c, w.q, c->pf_xn, T, c->pf_qr, n, 0);
-    enq_gemm(c, w.k, c->pf_xn, T, c->pf_kr, kv, 0);
-    enq_gemm(c, w.v, c->pf_xn, T, c->pf_vr, kv, 0);
+    enq_gemm(c, {{w.q, c->pf_qr, n}, {w.k, c->pf_kr, kv}, {w.v, c->pf_vr, kv}}, c->pf_xn, T, 0);
     hipLaunchKernelGGL(k_pf_rope_kv, dim3((std::max(n, kv) + 255) / 256, T), dim3(256), 0, c->stream, c->pf_qr,
                        c->pf_kr, c->pf_vr, c->pf_q, c->kc[l], c->vc[l], c->rope, p0, n, cf.n_head, c->hd, kv);
     enq_pf_attn(c, l, T, p0);
-    enq_gemm(c, w.o, c->pf_att, T, c->pf_x, n, 1);
+    enq_gemm(c, {{w.o, c->pf_x, n}}, c->pf_att, T, 1);
     hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.fn, cf.rms_eps, n, c->pf_xn);
-    enq_gemm(c, w.g, c->pf_xn, T, c->pf_g, ff, 0);
-    enq_gemm(c, w.u, c->pf_xn, T, c->pf_u, ff, 0);
+    enq_gemm(c, {{w.g, c->pf_g, ff}, {w.u, c->pf_u, ff}}, c->pf_xn, T, 0);
     const size_t cnt = (size_t)T * ff;
     hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, c->stream, c->pf_g, c->pf_u,
                        c->pf_h, cnt);
-    enq_gemm(c, w.d, c->pf_h, T, c->pf_x, n, 1);
+    enq_gemm(c, {{w.d, c->pf_x, n}}, c->pf_h, T, 1);
   }
   HIPCHK(c, hipGetLastError());
   return TALOS_OK;
