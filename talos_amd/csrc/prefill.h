@@ -284,15 +284,22 @@ struct PfAttn {
   float scale;       // 1 / sqrt(hd)
 };
 
-template <int HD>
-__global__ __launch_bounds__(512) void k_pf_attn(PfAttn A) {
+// NT threads (max(4, group) waves, rounded to 4 or 8); the block's K/V tile
+// for positions j0 .. j0 + 63 is fetched as float4 (16 per position and
+// array at HD = 64 ...), C per thread, into registers one tile ahead of the
+// tile being computed, then written to LDS between two block syncs.
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
   constexpr int KP = HD + 4, VP = HD + 16;  // LDS pitches: conflict-free A reads of K and of V
+  constexpr int F4 = PF_ATT_KT * HD / 4;    // float4 per tile and array
+  constexpr int C = (F4 + NT - 1) / NT;     // per thread
   extern __shared__ float sm[];
   float* Ks = sm;                   // [64][KP]
   float* Vs = sm + PF_ATT_KT * KP;  // [64][VP]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const uint32_t kvh = blockIdx.x, t0 = blockIdx.y * PF_ATT_Q;
+  // the latest queries (the longest causal loops) go out first
+  const uint32_t kvh = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * PF_ATT_Q;
   const uint32_t h = kvh * A.group + (uint32_t)wave;  // this wave's q head
   const bool live = (uint32_t)wave < A.group;
   const uint32_t tq = t0 + li;                         // this lane's query (B column)
@@ -311,16 +318,39 @@ __global__ __launch_bounds__(512) void k_pf_attn(PfAttn A) {
   float m = -INFINITY, l = 0.f;
   // positions 0 .. last, last = the block's largest query position
   const int last = (int)(A.p0 + min(t0 + PF_ATT_Q, A.T) - 1);
-  const int nthreads = blockDim.x;
-  for (int j0 = 0; j0 <= last; j0 += PF_ATT_KT) {
-    __syncthreads();
-    for (int i = tid; i < PF_ATT_KT * HD; i += nthreads) {
-      const int pj = i / HD, d = i % HD, j = j0 + pj;
-      const bool ok = j <= last;
-      Ks[pj * KP + d] = ok ? A.kc[(size_t)j * A.kv_dim + (size_t)kvh * HD + d] : 0.f;
-      Vs[pj * VP + d] = ok ? A.vc[(size_t)j * A.kv_dim + (size_t)kvh * HD + d] : 0.f;
+  const float* kbase = A.kc + (size_t)kvh * HD;
+  const float* vbase = A.vc + (size_t)kvh * HD;
+  f4 kr[C], vr[C];
+  // float4 e of a tile: position e / (HD / 4), dims 4 (e % (HD / 4)) .. +3;
+  // positions past `last` (and e past the tile) read a clamped row and are
+  // zeroed when stored
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int e = tid + NT * c, pj = e / (HD / 4), d4 = e % (HD / 4);
+      const int j = min(j0 + min(pj, PF_ATT_KT - 1), last);
+      kr[c] = *reinterpret_cast<const f4*>(kbase + (size_t)j * A.kv_dim + 4 * d4);
+      vr[c] = *reinterpret_cast<const f4*>(vbase + (size_t)j * A.kv_dim + 4 * d4);
     }
+  };
+  auto put = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int e = tid + NT * c, pj = e / (HD / 4), d4 = e % (HD / 4);
+      if (e < F4) {
+        const bool ok = j0 + pj <= last;
+        const f4 z{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f4*>(Ks + pj * KP + 4 * d4) = ok ? kr[c] : z;
+        *reinterpret_cast<f4*>(Vs + pj * VP + 4 * d4) = ok ? vr[c] : z;
+      }
+    }
+  };
+  fetch(0);
+  for (int j0 = 0; j0 <= last; j0 += PF_ATT_KT) {
+    __syncthreads();  // the previous tile's reads of Ks / Vs are done
+    put(j0);
     __syncthreads();
+    fetch(j0 + PF_ATT_KT <= last ? j0 + PF_ATT_KT : j0);  // the next tile's rows in flight
     if (!live) continue;
     // S^T for the four 16-position sub-tiles
     pf4 st[4];

@@ -1047,11 +1047,15 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
   A.hd = c->hd;
   A.group = c->group;
   A.scale = 1.0f / sqrtf((float)c->hd);
-  const dim3 grid(c->cfg.n_head_kv, (T + PF_ATT_Q - 1) / PF_ATT_Q), block(64 * c->group);
+  const bool wide = c->group > 4 || c->hd > 128;  // 8 waves, else 4
+  const dim3 grid(c->cfg.n_head_kv, (T + PF_ATT_Q - 1) / PF_ATT_Q), block(wide ? 512 : 256);
   const size_t lds = (size_t)PF_ATT_KT * (2 * c->hd + 20) * 4;
   switch (c->hd / 16) {
-#define PF_ATT_CASE(N) \
-  case N: hipLaunchKernelGGL(k_pf_attn<16 * N>, grid, block, lds, c->stream, A); break;
+#define PF_ATT_CASE(N)                                                                       \
+  case N:                                                                                    \
+    if (wide) hipLaunchKernelGGL((k_pf_attn<16 * N, 512>), grid, block, lds, c->stream, A); \
+    else hipLaunchKernelGGL((k_pf_attn<16 * N, 256>), grid, block, lds, c->stream, A);      \
+    break;
     PF_ATT_CASE(1) PF_ATT_CASE(2) PF_ATT_CASE(3) PF_ATT_CASE(4) PF_ATT_CASE(5) PF_ATT_CASE(6) PF_ATT_CASE(7)
     PF_ATT_CASE(8) PF_ATT_CASE(9) PF_ATT_CASE(10) PF_ATT_CASE(11) PF_ATT_CASE(12) PF_ATT_CASE(13) PF_ATT_CASE(14)
     PF_ATT_CASE(15) PF_ATT_CASE(16)
@@ -1061,7 +1065,9 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
 }
 
 void set_pf_attn_lds(int bytes) {
-#define PF_ATT_SET(N) set_max_lds((const void*)k_pf_attn<16 * N>, bytes);
+#define PF_ATT_SET(N)                                        \
+  set_max_lds((const void*)k_pf_attn<16 * N, 256>, bytes); \
+  set_max_lds((const void*)k_pf_attn<16 * N, 512>, bytes);
   PF_ATT_SET(1) PF_ATT_SET(2) PF_ATT_SET(3) PF_ATT_SET(4) PF_ATT_SET(5) PF_ATT_SET(6) PF_ATT_SET(7) PF_ATT_SET(8)
   PF_ATT_SET(9) PF_ATT_SET(10) PF_ATT_SET(11) PF_ATT_SET(12) PF_ATT_SET(13) PF_ATT_SET(14) PF_ATT_SET(15)
   PF_ATT_SET(16)
