@@ -17,8 +17,10 @@ def _step(msg):
     print(f"\n[prefill] {msg}", flush=True)
 
 
-@pytest.mark.parametrize("which,n,tol", [("tiny_f32", 8, 1e-4), ("gqa_q8", 16, 1e-3), ("mistral7b_q4", 32, 1e-3)])
+@pytest.mark.parametrize("which,n,tol", [("tiny_f32", 8, 1e-4), ("gqa_q8", 16, 1e-3), ("mistral7b_q4", 32, 1e-3),
+                                         ("tiny_f32", 200, 1e-4), ("gqa_q8", 300, 1e-3), ("mistral7b_q4", 136, 1e-3)])
 def test_batched_prefill_matches_oracle(talos, oracle, which, n, tol):
+    """Prompts of one to a few 64-token GEMM tiles, the last one partial."""
     from talos_amd import configs
     wl = getattr(configs, which)() if which != "mistral7b_q4" else configs.mistral7b_q4(ctx=256)
     _step(f"{which}: {n}-token prompt")
