@@ -205,7 +205,9 @@ def main() -> int:
     cus = model.bench_copy(copy_bytes, 10)
     copy_gbs = 2 * copy_bytes / (cus * 1e-6) / 1e9
     log(f"device copy of 1 GiB: {cus:.1f} us -> {copy_gbs:.0f} GB/s (read + write)")
-    phases = phase_breakdown(model.phase_timeline(int(toks[args.steps // 2 - 1]), mid), spec.n_layer)
+    # per-phase marks exist only in the persistent kernel
+    phases = (phase_breakdown(model.phase_timeline(int(toks[args.steps // 2 - 1]), mid), spec.n_layer)
+              if model.path() == "persistent" else None)
     log(f"phase us per layer: {phases}")
 
     # The host-buffer boundary (talos_hip_forward: embedding row in, logits
@@ -286,6 +288,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
+        "path": model.path(),
         "config": {"workload": "mistral7b_q4: dim 4096, 32 layers, 32 heads (hd 128), 8 KV heads, "
                                "FFN 14336, vocab 32000, RoPE 1e6, Q4_0 matrices + Q6_K output, "
                                "random 32-token prompt then greedy decode, KV ctx 4096",
@@ -444,7 +447,8 @@ def run_lc(args) -> int:
     us, sbytes = model.bench_token(int(toks[steps // 2 - 1]), mid, 16)
     k_gbs = sbytes / (us * 1e-6) / 1e9
     log(f"decode step at pos {mid}: {us:.1f} us, {sbytes / 1e6:.1f} MB -> {k_gbs:.0f} GB/s")
-    phases = phase_breakdown(model.phase_timeline(int(toks[steps // 2 - 1]), mid), spec.n_layer)
+    phases = (phase_breakdown(model.phase_timeline(int(toks[steps // 2 - 1]), mid), spec.n_layer)
+              if model.path() == "persistent" else None)
     log(f"phase us per layer: {phases}")
     wbytes = configs.bytes_per_token_weights(spec)
     kvpos = configs.kv_bytes_per_position(spec)

@@ -61,6 +61,24 @@ __device__ __forceinline__ DevMat pick3(const DevMat& a, const DevMat& b, const 
   return s == 0 ? a : (s == 1 ? b : c);
 }
 
+// x staging of the graph-path matvec kernels, a template policy: XF32 keeps
+// f32 x in LDS (carve_x / stage_x_then, every format); rows_iq.h's
+// XPlanes<NR> stages int8 planes for the v_dot4 engine (Q4_0 / Q8_0).
+struct XF32 {
+  XStage X;
+  int need;
+  __device__ __forceinline__ XF32(float* smem, int n, int need_) : X(carve_x(smem, n, need_)), need(need_) {}
+  template <class After>
+  __device__ __forceinline__ void stage(const float* x, int n, const float* w, float eps, bool norm,
+                                        After after) const {
+    stage_x_then(x, n, w, eps, norm, X.xs[0], X.xs[1], X.xsum, X.red, need & 1, need & 2, after);
+  }
+  template <uint32_t FMT>
+  __device__ __forceinline__ XF src() const {
+    return XF{X.xs[MvT<FMT>::L], X.xsum};
+  }
+};
+
 // ---------------------------------------------------------------- k_qkv --
 // rmsnorm(x, attn_norm) -> q/k/v rows -> RoPE(q, k) -> q buffer and the K/V
 // cache row at `pos` (src/model/llama.rs:118-130, src/math/ops.rs:48-61).
@@ -82,10 +100,10 @@ struct QKVParams {
   int need;
 };
 
-template <uint32_t FMT, int R, int U>
+template <uint32_t FMT, int R, int U, class XP = XF32>
 __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
   extern __shared__ float smem[];
-  const XStage X = carve_x(smem, P.n, P.need);
+  const XP X(smem, (int)P.n, P.need);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t total = P.units[0] + P.units[1] + P.units[2];
   const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
@@ -114,7 +132,7 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
     rmax = A0.rows;
   };
   auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
-    stage_x_then(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2, pf);
+    X.stage(P.x, (int)P.n, P.norm_w, P.eps, true, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     if (lane != 0) return;
@@ -141,7 +159,7 @@ __global__ __launch_bounds__(256) void k_qkv(QKVParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.template src<FMT>(), lane, true);
 }
 
 // --------------------------------------------------------------- k_rows --
@@ -162,10 +180,10 @@ struct RowParams {
   int need;
 };
 
-template <uint32_t FMT, int R, int U>
+template <uint32_t FMT, int R, int U, class XP = XF32>
 __global__ __launch_bounds__(256) void k_rows(RowParams P) {
   extern __shared__ float smem[];
-  const XStage X = carve_x(smem, P.n, P.need);
+  const XP X(smem, (int)P.n, P.need);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
   const int nunits = ubase >= P.units ? 0 : (int)min(P.upw, P.units - ubase);
@@ -176,8 +194,7 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
     rmax = P.m.rows;
   };
   auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
-    stage_x_then(P.x, P.n, P.norm_w, P.eps, P.norm_w != nullptr, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1,
-                 P.need & 2, pf);
+    X.stage(P.x, (int)P.n, P.norm_w, P.eps, P.norm_w != nullptr, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     const uint32_t r0 = (ubase + k) * R;
@@ -190,7 +207,7 @@ __global__ __launch_bounds__(256) void k_rows(RowParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
+  mv_stream<FMT, R, U, false>(nunits, unit, [] {}, stage, epi, X.template src<FMT>(), lane, true);
 }
 
 // ------------------------------------------------------------- k_gateup --
@@ -209,10 +226,10 @@ struct GateUpParams {
   int need;
 };
 
-template <uint32_t FMT, int R, int U>
+template <uint32_t FMT, int R, int U, class XP = XF32>
 __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
   extern __shared__ float smem[];
-  const XStage X = carve_x(smem, P.n, P.need);
+  const XP X(smem, (int)P.n, P.need);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t ubase = (blockIdx.x * 4 + wave) * P.upw;
   const int nunits = ubase >= P.units ? 0 : (int)min(P.upw, P.units - ubase);
@@ -224,7 +241,7 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
     rmax = P.g.rows;
   };
   auto stage = [&](auto&& pf) {  // x loads, then the first weight loads, then the staging
-    stage_x_then(P.x, P.n, P.norm_w, P.eps, true, X.xs[0], X.xs[1], X.xsum, X.red, P.need & 1, P.need & 2, pf);
+    X.stage(P.x, (int)P.n, P.norm_w, P.eps, true, pf);
   };
   auto epi = [&](int k, const float(&y)[R]) {
     const uint32_t p0 = (ubase + k) * PR;
@@ -237,7 +254,7 @@ __global__ __launch_bounds__(256) void k_gateup(GateUpParams P) {
       }
     }
   };
-  mv_stream<FMT, R, U, true>(nunits, unit, [] {}, stage, epi, XF{X.xs[MvT<FMT>::L], X.xsum}, lane, true);
+  mv_stream<FMT, R, U, true>(nunits, unit, [] {}, stage, epi, X.template src<FMT>(), lane, true);
 }
 
 // ---------------------------------------------------------------- k_attn --

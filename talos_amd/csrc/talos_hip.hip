@@ -312,6 +312,13 @@ int need_norm(talos_hip_ctx* c, const std::string& name, size_t n, const float**
 
 int layout_need(uint32_t fmt) { return 1 << fmt_xlayout(fmt); }
 
+// Staging rounds of the int8-plane x for a matvec over rows n long in
+// format fmt, or 0 for f32 x (other formats, n beyond the planes,
+// TALOS_HIP_DOT4=0).
+int iq_rounds(const talos_hip_ctx* c, uint32_t fmt, size_t n) {
+  return c->allow_dot4 && (fmt == TALOS_FMT_Q4_0 || fmt == TALOS_FMT_Q8_0) ? rows_iq_rounds(n) : 0;
+}
+
 // Instantiate KERN<format, rows-per-unit, U> for the runtime (fmt, U) pair.
 #define TALOS_MV_U(KERN, F, U, ...)                                      \
   do {                                                                   \
@@ -327,6 +334,25 @@ int layout_need(uint32_t fmt) { return 1 << fmt_xlayout(fmt); }
       case TALOS_FMT_Q8_0: TALOS_MV_U(KERN, TALOS_FMT_Q8_0, U, __VA_ARGS__); break; \
       default: TALOS_MV_U(KERN, TALOS_FMT_Q6_K, U, __VA_ARGS__); break;       \
     }                                                                         \
+  } while (0)
+
+// KERN<F, mv_rows(F), U, XPlanes<NR>>: the int8-plane x staging for a
+// Q4_0 / Q8_0 matrix whose rows are n long, NR = rows_iq_rounds(n).
+#define TALOS_MV_IQ_NR(KERN, F, U_, nr, ...)                                                \
+  do {                                                                                      \
+    if ((nr) == 2) hipLaunchKernelGGL((KERN<F, mv_rows(F), U_, XPlanes<2>>), __VA_ARGS__); \
+    else hipLaunchKernelGGL((KERN<F, mv_rows(F), U_, XPlanes<8>>), __VA_ARGS__);           \
+  } while (0)
+#define TALOS_MV_IQ_U(KERN, F, U, nr, ...)                             \
+  do {                                                                 \
+    if ((U) >= 4) TALOS_MV_IQ_NR(KERN, F, 4, nr, __VA_ARGS__);        \
+    else if ((U) == 2) TALOS_MV_IQ_NR(KERN, F, 2, nr, __VA_ARGS__);   \
+    else TALOS_MV_IQ_NR(KERN, F, 1, nr, __VA_ARGS__);                 \
+  } while (0)
+#define TALOS_MV_LAUNCH_IQ(KERN, fmt, U, nr, ...)                                             \
+  do {                                                                                        \
+    if ((fmt) == TALOS_FMT_Q4_0) TALOS_MV_IQ_U(KERN, TALOS_FMT_Q4_0, U, nr, __VA_ARGS__);     \
+    else TALOS_MV_IQ_U(KERN, TALOS_FMT_Q8_0, U, nr, __VA_ARGS__);                             \
   } while (0)
 
 // Let kernel k take up to `bytes` of LDS in all (dynamic plus its own static
@@ -450,8 +476,12 @@ void enq_qkv(talos_hip_ctx* c, uint32_t l, const LayerW& w) {
   P.need = layout_need(w.q->mat.fmt) | layout_need(w.k->mat.fmt) | layout_need(w.v->mat.fmt);
   uint32_t blocks;
   plan(P.units[0] + P.units[1] + P.units[2], P.upw, blocks);
-  TALOS_MV_LAUNCH(k_qkv, w.q->mat.fmt, mv_u(w.q->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, P.need),
-                  c->stream, P);
+  if (const int nr = iq_rounds(c, w.q->mat.fmt, n))
+    TALOS_MV_LAUNCH_IQ(k_qkv, w.q->mat.fmt, mv_u(w.q->mat.nchunk), nr, dim3(blocks), dim3(256), rows_iq_lds_bytes(n),
+                       c->stream, P);
+  else
+    TALOS_MV_LAUNCH(k_qkv, w.q->mat.fmt, mv_u(w.q->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, P.need),
+                    c->stream, P);
 }
 
 // The layer forms the graph path can fuse: q/k/v in one kernel with RoPE in
@@ -483,8 +513,12 @@ void enq_rows(talos_hip_ctx* c, const DevWeight* w, const float* x, uint32_t n, 
   R.need = layout_need(w->mat.fmt);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
-                  c->stream, R);
+  if (const int nr = iq_rounds(c, w->mat.fmt, n))
+    TALOS_MV_LAUNCH_IQ(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), nr, dim3(blocks), dim3(256), rows_iq_lds_bytes(n),
+                       c->stream, R);
+  else
+    TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
+                    c->stream, R);
 }
 
 // q/k/v of different formats or shapes the fused epilogue does not take:
@@ -557,8 +591,12 @@ void enq_resid(talos_hip_ctx* c, const DevWeight* w, const float* x, uint32_t n,
   R.need = layout_need(w->mat.fmt);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
-                  c->stream, R);
+  if (const int nr = iq_rounds(c, w->mat.fmt, n))
+    TALOS_MV_LAUNCH_IQ(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), nr, dim3(blocks), dim3(256), rows_iq_lds_bytes(n),
+                       c->stream, R);
+  else
+    TALOS_MV_LAUNCH(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), dim3(blocks), dim3(256), stage_lds_bytes(n, R.need),
+                    c->stream, R);
 }
 
 void enq_gateup(talos_hip_ctx* c, const LayerW& w) {
@@ -575,8 +613,12 @@ void enq_gateup(talos_hip_ctx* c, const LayerW& w) {
   G.need = layout_need(w.g->mat.fmt) | layout_need(w.u->mat.fmt);
   uint32_t blocks;
   plan(G.units, G.upw, blocks);
-  TALOS_MV_LAUNCH(k_gateup, w.g->mat.fmt, mv_u(w.g->mat.nchunk), dim3(blocks), dim3(256),
-                  stage_lds_bytes(G.n, G.need), c->stream, G);
+  if (const int nr = iq_rounds(c, w.g->mat.fmt, G.n))
+    TALOS_MV_LAUNCH_IQ(k_gateup, w.g->mat.fmt, mv_u(w.g->mat.nchunk), nr, dim3(blocks), dim3(256),
+                       rows_iq_lds_bytes(G.n), c->stream, G);
+  else
+    TALOS_MV_LAUNCH(k_gateup, w.g->mat.fmt, mv_u(w.g->mat.nchunk), dim3(blocks), dim3(256),
+                    stage_lds_bytes(G.n, G.need), c->stream, G);
 }
 
 void enq_output(talos_hip_ctx* c, const DevWeight* wout, const float* onorm) {
@@ -592,8 +634,12 @@ void enq_output(talos_hip_ctx* c, const DevWeight* wout, const float* onorm) {
   R.need = layout_need(wout->mat.fmt);
   uint32_t blocks;
   plan(R.units, R.upw, blocks);
-  TALOS_MV_LAUNCH(k_rows, wout->mat.fmt, mv_u(wout->mat.nchunk), dim3(blocks), dim3(256),
-                  stage_lds_bytes(R.n, R.need), c->stream, R);
+  if (const int nr = iq_rounds(c, wout->mat.fmt, R.n))
+    TALOS_MV_LAUNCH_IQ(k_rows, wout->mat.fmt, mv_u(wout->mat.nchunk), nr, dim3(blocks), dim3(256),
+                       rows_iq_lds_bytes(R.n), c->stream, R);
+  else
+    TALOS_MV_LAUNCH(k_rows, wout->mat.fmt, mv_u(wout->mat.nchunk), dim3(blocks), dim3(256),
+                    stage_lds_bytes(R.n, R.need), c->stream, R);
 }
 
 // Enqueue one token step on the stream.
@@ -1671,31 +1717,10 @@ static int enqueue_matvec(talos_hip_ctx* c, const DevWeight* w, const float* d_x
     HIPCHK(c, hipGetLastError());
     return TALOS_OK;
   }
-  const int nr = rows_iq_rounds(w->cols);
-  if ((w->mat.fmt == TALOS_FMT_Q4_0 || w->mat.fmt == TALOS_FMT_Q8_0) && nr && c->allow_dot4) {
+  if (const int nr = iq_rounds(c, w->mat.fmt, w->cols)) {
     plan(R.units, R.upw, blocks);
-    const size_t lq = rows_iq_lds_bytes(w->cols);
-    const int u = mv_u(w->mat.nchunk);
-#define IQ_NR(F, U_)                                                                                       \
-  do {                                                                                                     \
-    constexpr int RR = mv_rows(F);                                                                         \
-    switch (nr) {                                                                                          \
-      case 1: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 1>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
-      case 2: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 2>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
-      case 4: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 4>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
-      default: hipLaunchKernelGGL((k_rows_iq<F, RR, U_, 8>), dim3(blocks), dim3(256), lq, c->stream, R); break; \
-    }                                                                                                      \
-  } while (0)
-#define IQ_U(F)                   \
-  do {                            \
-    if (u >= 4) IQ_NR(F, 4);      \
-    else if (u == 2) IQ_NR(F, 2); \
-    else IQ_NR(F, 1);             \
-  } while (0)
-    if (w->mat.fmt == TALOS_FMT_Q4_0) IQ_U(TALOS_FMT_Q4_0);
-    else IQ_U(TALOS_FMT_Q8_0);
-#undef IQ_U
-#undef IQ_NR
+    TALOS_MV_LAUNCH_IQ(k_rows, w->mat.fmt, mv_u(w->mat.nchunk), nr, dim3(blocks), dim3(256),
+                       rows_iq_lds_bytes(w->cols), c->stream, R);
     HIPCHK(c, hipGetLastError());
     return TALOS_OK;
   }
