@@ -237,6 +237,168 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(PfGemm G) {
   }
 }
 
+// ------------------------------------------------- the split-f16 GEMM --
+// The same product for Q4_0 / Q8_0 weights on v_mfma_f32_16x16x32_f16.  A
+// quantized weight is an integer (Q8_0 q in [-128, 127], Q4_0 nib - 8 in
+// [-8, 7]) times its block's f16 scale d, and the integers are exact in f16;
+// x is split as hi = f16(x), lo = f16(x - hi), which carries x to within
+// 2^-22 of itself (f32 level).  Per 32-element block one MFMA pair forms
+// sum_k q_k (hi_k + lo_k) exactly in f32 (f16 products are exact), and the
+// block adds d times it to the f32 accumulator: the reference's f32 products
+// d q x summed in another order, so within f32 rounding of it.  One MFMA
+// covers one quant block (K = 32): lane l supplies A[token l % 16][k = 8
+// (l / 16) .. +7] and B[k = 8 (l / 16) .. +7][row l % 16], the same k set in
+// both, and holds D[token 4 (l / 16) + r][row l % 16] in register r.
+// Tile, waves and pipelining as k_pf_gemm; X is staged in LDS as the hi and
+// lo halves, [token][k] with a pitch of 72 halves.
+typedef _Float16 pfh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pfh2 __attribute__((ext_vector_type(2)));
+#define PF_HP 72
+
+__device__ __forceinline__ pf4 mfma16x32h(pfh8 a, pfh8 b, pf4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// This lane's 8 weights of each of the chunk's two blocks as raw bytes (8
+// per block: Q8_0 quants q + 128, or Q4_0 bytes whose low or high nibbles
+// are the elements), with the two blocks' f16 scales.
+struct PfW16 {
+  uint32_t q[2][2];
+  uint32_t d;
+};
+template <uint32_t FMT>
+__device__ __forceinline__ void pf16_load_w(PfW16& F, const DevMat& W, uint32_t rowc, uint32_t k0, uint32_t K,
+                                            int g) {
+  const uint32_t nb = K / 32;
+  uint32_t dd[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const uint32_t bi0 = (k0 + 32 * blk) / 32, bi = bi0 < nb ? bi0 : nb - 1;
+    const size_t ci = (size_t)rowc * nb + bi;
+    // Q8_0: elements 8 g .. +7 are bytes 8 g .. +7; Q4_0: bytes 8 (g & 1) .. +7,
+    // low nibbles for g < 2 (elements j), high for g >= 2 (elements j + 16)
+    const uint8_t* src = FMT == TALOS_FMT_Q8_0 ? W.q + ci * 32 + 8 * g : W.q + ci * 16 + 8 * (g & 1);
+    const uint2 v = *reinterpret_cast<const uint2*>(src);
+    F.q[blk][0] = v.x;
+    F.q[blk][1] = v.y;
+    dd[blk] = W.d[ci];
+  }
+  F.d = dd[0] | (dd[1] << 16);
+}
+// The 8 weights of block blk as f16 integers (zero past K): each byte b
+// (a Q8_0 q + 128, or a Q4_0 nibble) becomes the half 1024 + b by placing
+// 0x64 above it, then the offset is subtracted (exact in f16).
+template <uint32_t FMT>
+__device__ __forceinline__ pfh8 pf16_weights(const PfW16& F, int blk, int g, bool live) {
+  const float off = FMT == TALOS_FMT_Q8_0 ? 1152.f : 1032.f;
+  const pfh2 o2{(_Float16)off, (_Float16)off};
+  pfh8 r;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    uint32_t v = F.q[blk][w];
+    if (FMT == TALOS_FMT_Q4_0) v = (g >= 2 ? v >> 4 : v) & 0x0F0F0F0Fu;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u);
+    const pfh2 a = __builtin_bit_cast(pfh2, lo) - o2, b = __builtin_bit_cast(pfh2, hi) - o2;
+    r[4 * w + 0] = a[0];
+    r[4 * w + 1] = a[1];
+    r[4 * w + 2] = b[0];
+    r[4 * w + 3] = b[1];
+  }
+  return live ? r : pfh8{0, 0, 0, 0, 0, 0, 0, 0};
+}
+
+// X[tb .. +64][k0 .. +64]: thread t holds token t / 8, elements k0 + 8 (t % 8)
+// .. +7 (zero past T and K).
+struct PfX16 {
+  f4 v[2];
+};
+__device__ __forceinline__ void pf16_load_x(PfX16& P, const float* __restrict__ X, uint32_t T, uint32_t K,
+                                            uint32_t tb, uint32_t k0, int tid) {
+  const uint32_t t = tb + (uint32_t)(tid >> 3), k = k0 + 8u * (uint32_t)(tid & 7);
+  const uint32_t tc = t < T ? t : T - 1, kc = k < K ? k : K - 8;
+  const float* p = X + (size_t)tc * K + kc;
+  const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+  const bool ok = t < T && k < K;
+  const f4 z{0.f, 0.f, 0.f, 0.f};
+  P.v[0] = ok ? a : z;
+  P.v[1] = ok ? b : z;
+}
+__device__ __forceinline__ void pf16_store_x(const PfX16& P, _Float16* Xh, _Float16* Xl, int tid) {
+  const int tt = tid >> 3, k8 = tid & 7;
+  const float x[8] = {P.v[0].x, P.v[0].y, P.v[0].z, P.v[0].w, P.v[1].x, P.v[1].y, P.v[1].z, P.v[1].w};
+  pfh8 h, l;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h[i] = (_Float16)x[i];
+    l[i] = (_Float16)(x[i] - (float)h[i]);
+  }
+  *reinterpret_cast<pfh8*>(Xh + tt * PF_HP + 8 * k8) = h;
+  *reinterpret_cast<pfh8*>(Xl + tt * PF_HP + 8 * k8) = l;
+}
+
+template <uint32_t FMT>
+__global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
+  static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "integer weights only");
+  __shared__ _Float16 Xs[2][2][64 * PF_HP];  // [buffer][hi, lo][token][k]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  uint32_t tile = blockIdx.x, s = 0;
+  while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
+  const PfSeg& S = G.S[s];
+  const uint32_t M = S.W.rows;
+  const uint32_t tb = blockIdx.y * 64;
+  const uint32_t row = tile * PF_ROWS + (uint32_t)wave * 16 + li;
+  const uint32_t rowc = row < M ? row : M - 1;
+  pf4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = pf4{0.f, 0.f, 0.f, 0.f};
+  const int nchunks = (int)((G.K + PF_KC - 1) / PF_KC);
+  PfW16 wc, wn;
+  PfX16 xc, xn;
+  pf16_load_w<FMT>(wc, S.W, rowc, 0, G.K, g);
+  pf16_load_x(xc, G.X, G.T, G.K, tb, 0, tid);
+  for (int c = 0; c < nchunks; ++c) {
+    _Float16* Xh = Xs[c & 1][0];
+    _Float16* Xl = Xs[c & 1][1];
+    pf16_store_x(xc, Xh, Xl, tid);
+    __syncthreads();
+    const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
+    pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
+    pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const bool live = k0 + 32 * blk < G.K;
+      const pfh8 b = pf16_weights<FMT>(wc, blk, g, live);
+      const float d = f16_to_f32((uint16_t)(wc.d >> (16 * blk)));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int off = (16 * t + li) * PF_HP + 32 * blk + 8 * g;
+        const pfh8 ah = *reinterpret_cast<const pfh8*>(Xh + off);
+        const pfh8 al = *reinterpret_cast<const pfh8*>(Xl + off);
+        pf4 blkacc = mfma16x32h(ah, b, pf4{0.f, 0.f, 0.f, 0.f});
+        blkacc = mfma16x32h(al, b, blkacc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(d, blkacc[r], acc[t][r]);
+      }
+    }
+    wc = wn;
+    xc = xn;
+  }
+  if (row < M) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t tok = tb + 16 * t + 4 * g + r;
+        if (tok < G.T) {
+          float* y = S.Y + (size_t)tok * S.ldy + row;
+          *y = G.accumulate ? *y + acc[t][r] : acc[t][r];
+        }
+      }
+  }
+}
+
 // RoPE of the raw q and k rows of T tokens at positions p0 + t (any
 // head_dim, as k_rope_qkv), the K and V rows into the cache.
 __global__ __launch_bounds__(256) void k_pf_rope_kv(const float* __restrict__ Qr, const float* __restrict__ Kr,

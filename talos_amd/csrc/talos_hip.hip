@@ -127,6 +127,7 @@ struct talos_hip_ctx {
   float *pf_kr = nullptr, *pf_vr = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_h = nullptr;
   int32_t* pf_tok = nullptr;
   bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
+  bool pf_f16 = true;       // TALOS_HIP_PF16=0: Q4_0/Q8_0 prefill GEMMs on f32 MFMA instead of split f16
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -1073,8 +1074,14 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float
     }
     const dim3 grid(tiles, (T + PF_TOK - 1) / PF_TOK);
     switch (type) {
-      case TALOS_GGML_Q4_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G); break;
-      case TALOS_GGML_Q8_0: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G); break;
+      case TALOS_GGML_Q4_0:
+        if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        break;
+      case TALOS_GGML_Q8_0:
+        if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        break;
       default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(PF_NT), 0, c->stream, G); break;
     }
   }
@@ -1207,6 +1214,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_dsplit = env && (env[0] == '0' || env[0] == '1') ? env[0] - '0' : 2;
   env = getenv("TALOS_HIP_BATCH");
   c->allow_batch = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_PF16");
+  c->pf_f16 = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
