@@ -368,7 +368,9 @@ def lc_measure(args) -> dict:
     t = time.perf_counter()
     _, first = model.prefill(prefix, 0, want_logits=False)
     prefill_s = time.perf_counter() - t
-    log(f"lc: prefill of {P} positions {prefill_s:.2f}s ({P / prefill_s:.0f} tok/s)")
+    gemm_f, attn_f = configs.prefill_flops(spec, P)
+    log(f"lc: prefill of {P} positions {prefill_s:.2f}s ({P / prefill_s:.0f} tok/s, "
+        f"{(gemm_f + attn_f) / prefill_s / 1e12:.0f} TFLOP/s)")
     model.decode_greedy(first, P, 8)
     t0 = time.perf_counter()
     toks = model.decode_greedy(first, P, steps)
@@ -383,6 +385,11 @@ def lc_measure(args) -> dict:
     res = {"workload": f"mistral7b_q8_long: 7B shape, Q8_0 matrices, {P}-token uniform random prompt "
                        f"(talos_hip_prefill), {steps} greedy steps", "tok_s": round(steps / dt, 2), "steps": steps,
            "prefill_tok_s": round(P / prefill_s, 1),
+           "prefill": {"seconds": round(prefill_s, 3), "projection_flops": gemm_f, "attention_flops": attn_f,
+                       "achieved_tflops": round((gemm_f + attn_f) / prefill_s / 1e12, 1),
+                       "note": "projections on f16 matrix cores with x split into two halves (peak 2500 "
+                               "TFLOP/s per f16 MFMA, two per product), attention on f32 matrix cores "
+                               "(157.3 TFLOP/s)"},
            "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(k_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": int(sbytes),
                         "us_per_launch": round(us, 2), "pos": mid},

@@ -71,6 +71,18 @@ def bytes_per_token_weights(spec: SynthSpec) -> int:
             + nbytes(1, c, spec.embd_type))
 
 
+def prefill_flops(spec: SynthSpec, n: int, p0: int = 0) -> tuple:
+    """(projection flops, attention flops) of a prompt of n tokens at
+    positions p0 .. p0 + n - 1: 2 per weight per token for the layer
+    matrices, and 4 * n_head * head_dim per (query, visible position) pair
+    for the scores and the weighted sum."""
+    c, ff, kv = spec.n_embd, spec.n_ff, spec.kv_dim
+    params = spec.n_layer * (2 * c * c + 2 * kv * c + 3 * ff * c)
+    pairs = sum(p0 + t + 1 for t in range(n))
+    hd = c // spec.n_head
+    return 2 * params * n, spec.n_layer * 4 * spec.n_head * hd * pairs
+
+
 def kv_bytes_per_position(spec: SynthSpec) -> int:
     """K and V bytes per cached position across all layers (f32)."""
     return spec.n_layer * 2 * spec.kv_dim * 4
