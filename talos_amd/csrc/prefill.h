@@ -259,6 +259,19 @@ __device__ __forceinline__ pf4 mfma16x32h(pfh8 a, pfh8 b, pf4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// hi + lo halves of v = a * b rounded to f32.  The empty asm statement pins
+// the rounded product in a register: otherwise the compiler may fold the
+// product into v_fma_mixlo_f16 (the exact product rounded once to f16) for
+// the hi that lo is computed from while converting the rounded f32 product
+// for the hi it stores, and where the two roundings differ (an f32 product
+// on an f16 rounding midpoint) hi + lo is off by an f16 ulp.
+__device__ __forceinline__ void pf16_split_product(float a, float b, _Float16& hi, _Float16& lo) {
+  float v = a * b;
+  asm volatile("" : "+v"(v));
+  hi = (_Float16)v;
+  lo = (_Float16)(v - (float)hi);
+}
+
 // This lane's 8 weights of each of the chunk's two blocks as raw bytes (8
 // per block: Q8_0 quants q + 128, or Q4_0 bytes whose low or high nibbles
 // are the elements), with the two blocks' f16 scales.
@@ -573,4 +586,203 @@ __global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) dst[16 * i + 4 * g + r] = o[i][r] * inv;
   }
+}
+
+// ------------------------------------------ split-f16 flash attention --
+// k_pf_attn on v_mfma_f32_16x16x32_f16 (head_dim a multiple of 32): K, V, q
+// and the probabilities split as hi + lo halves, each product as three
+// MFMAs (hi hi, hi lo, lo hi; the lo lo term is below 2^-22 of the product),
+// f32 accumulation.  The tile's K rows are converted as they are staged,
+// K as [position][dim] and V transposed, [dim][position], so that every
+// operand fragment is one 16-byte LDS read.  S^T sub-tile u = 2 b + e (16
+// positions) takes its A rows in the order pi(i) = 32 b + 8 (i / 4) + 4 e +
+// i % 4: lane l then holds, over sub-tiles 2 b and 2 b + 1, the scores of
+// positions 32 b + 8 (l / 16) .. +7 for query l % 16 -- exactly its B
+// fragment of P^T for the 32-position P.V step b.
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn A) {
+  static_assert(HD % 32 == 0, "head_dim a multiple of 32");
+  constexpr int KP = HD + 8;                  // K halves pitch
+  constexpr int VP = PF_ATT_KT + 8;           // transposed V halves pitch
+  constexpr int F4 = PF_ATT_KT * HD / 4;      // K float4 per tile
+  constexpr int CK = (F4 + NT - 1) / NT;      // ... per thread
+  constexpr int VQ = PF_ATT_KT / 2 * HD / 4;  // V (position pair, dim quad) per tile
+  constexpr int CV = (VQ + NT - 1) / NT;
+  extern __shared__ float sm[];
+  _Float16* Kh = reinterpret_cast<_Float16*>(sm);
+  _Float16* Kl = Kh + PF_ATT_KT * KP;
+  _Float16* Vh = Kl + PF_ATT_KT * KP;  // [HD][VP]
+  _Float16* Vl = Vh + HD * VP;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const uint32_t kvh = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * PF_ATT_Q;
+  const uint32_t h = kvh * A.group + (uint32_t)wave;
+  const bool live = (uint32_t)wave < A.group;
+  const uint32_t tq = t0 + li;
+  const int qpos = (int)(A.p0 + (tq < A.T ? tq : A.T - 1));
+  constexpr float kLog2e = 1.4426950408889634f;
+  // Q^T fragments of step s: Q[query li][32 s + 8 g .. +7], pre-scaled, split
+  pfh8 qh[HD / 32], ql[HD / 32];
+  {
+    const float* qrow = A.Q + (size_t)(tq < A.T ? tq : A.T - 1) * A.n + (size_t)(live ? h : 0) * HD;
+    const float sc = A.scale * kLog2e;
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+      const f4 a = *reinterpret_cast<const f4*>(qrow + 32 * s + 8 * g);
+      const f4 b = *reinterpret_cast<const f4*>(qrow + 32 * s + 8 * g + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        _Float16 hi, lo;
+        pf16_split_product(v[i], sc, hi, lo);
+        qh[s][i] = hi;
+        ql[s][i] = lo;
+      }
+    }
+  }
+  pf4 o[HD / 16];
+#pragma unroll
+  for (int i = 0; i < HD / 16; ++i) o[i] = pf4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  const int last = (int)(A.p0 + min(t0 + PF_ATT_Q, A.T) - 1);
+  const float* kbase = A.kc + (size_t)kvh * HD;
+  const float* vbase = A.vc + (size_t)kvh * HD;
+  f4 kr[CK], vr[CV][2];
+  // K float4 e: position e / (HD / 4), dims 4 (e % (HD / 4)) .. +3; V item e:
+  // positions 2 (e / (HD / 4)) and + 1, the same dims.  Rows past `last` (and
+  // items past the tile) read a clamped row and are zeroed when stored.
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < CK; ++c) {
+      const int e = tid + NT * c, pj = min(e / (HD / 4), PF_ATT_KT - 1), d4 = e % (HD / 4);
+      kr[c] = *reinterpret_cast<const f4*>(kbase + (size_t)min(j0 + pj, last) * A.kv_dim + 4 * d4);
+    }
+#pragma unroll
+    for (int c = 0; c < CV; ++c) {
+      const int e = tid + NT * c, pp = min(e / (HD / 4), PF_ATT_KT / 2 - 1), d4 = e % (HD / 4);
+#pragma unroll
+      for (int w = 0; w < 2; ++w)
+        vr[c][w] = *reinterpret_cast<const f4*>(vbase + (size_t)min(j0 + 2 * pp + w, last) * A.kv_dim + 4 * d4);
+    }
+  };
+  auto split2 = [](float a, float b, uint32_t& hi, uint32_t& lo) {
+    const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+    const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, ah) | ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16);
+  };
+  auto put = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < CK; ++c) {
+      const int e = tid + NT * c, pj = e / (HD / 4), d4 = e % (HD / 4);
+      if (e < F4) {
+        const f4 z{0.f, 0.f, 0.f, 0.f};
+        const f4 v = j0 + pj <= last ? kr[c] : z;
+        uint2 hi, lo;
+        split2(v.x, v.y, hi.x, lo.x);
+        split2(v.z, v.w, hi.y, lo.y);
+        *reinterpret_cast<uint2*>(Kh + pj * KP + 4 * d4) = hi;
+        *reinterpret_cast<uint2*>(Kl + pj * KP + 4 * d4) = lo;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CV; ++c) {
+      const int e = tid + NT * c, pp = e / (HD / 4), d4 = e % (HD / 4);
+      if (e < VQ) {
+        const f4 z{0.f, 0.f, 0.f, 0.f};
+        const f4 a = j0 + 2 * pp <= last ? vr[c][0] : z;
+        const f4 b = j0 + 2 * pp + 1 <= last ? vr[c][1] : z;
+        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t hi, lo;
+          split2(av[k], bv[k], hi, lo);
+          *reinterpret_cast<uint32_t*>(Vh + (4 * d4 + k) * VP + 2 * pp) = hi;
+          *reinterpret_cast<uint32_t*>(Vl + (4 * d4 + k) * VP + 2 * pp) = lo;
+        }
+      }
+    }
+  };
+  fetch(0);
+  for (int j0 = 0; j0 <= last; j0 += PF_ATT_KT) {
+    __syncthreads();
+    put(j0);
+    __syncthreads();
+    fetch(j0 + PF_ATT_KT <= last ? j0 + PF_ATT_KT : j0);
+    if (!live) continue;
+    pf4 st[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      st[u] = pf4{0.f, 0.f, 0.f, 0.f};
+      const int p = 32 * (u >> 1) + 8 * (li >> 2) + 4 * (u & 1) + (li & 3);  // pi(li) of sub-tile u
+#pragma unroll
+      for (int s = 0; s < HD / 32; ++s) {
+        const pfh8 kh = *reinterpret_cast<const pfh8*>(Kh + p * KP + 32 * s + 8 * g);
+        const pfh8 kl = *reinterpret_cast<const pfh8*>(Kl + p * KP + 32 * s + 8 * g);
+        st[u] = mfma16x32h(kh, qh[s], st[u]);
+        st[u] = mfma16x32h(kh, ql[s], st[u]);
+        st[u] = mfma16x32h(kl, qh[s], st[u]);
+      }
+    }
+    // register r of sub-tile u: position j0 + 32 (u / 2) + 8 g + 4 (u % 2) + r
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j0 + 32 * (u >> 1) + 8 * g + 4 * (u & 1) + r;
+        if (j > qpos) st[u][r] = -INFINITY;
+        mx = fmaxf(mx, st[u][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = st[u][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[u][r] - mn);
+        st[u][r] = pv;
+        ps += pv;
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i) o[i] *= alpha;
+    // O^T[dim][query] += V^T P^T over the two 32-position steps
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      pfh8 ph, pl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = st[2 * b + (i >> 2)][i & 3];
+        ph[i] = (_Float16)v;
+        pl[i] = (_Float16)(v - (float)ph[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < HD / 16; ++i) {
+        const pfh8 vh = *reinterpret_cast<const pfh8*>(Vh + (16 * i + li) * VP + 32 * b + 8 * g);
+        const pfh8 vl = *reinterpret_cast<const pfh8*>(Vl + (16 * i + li) * VP + 32 * b + 8 * g);
+        o[i] = mfma16x32h(vh, ph, o[i]);
+        o[i] = mfma16x32h(vh, pl, o[i]);
+        o[i] = mfma16x32h(vl, ph, o[i]);
+      }
+    }
+  }
+  if (live && tq < A.T) {
+    const float inv = 1.0f / l;
+    float* dst = A.out + (size_t)tq * A.n + (size_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < HD / 16; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[16 * i + 4 * g + r] = o[i][r] * inv;
+  }
+}
+
+static inline size_t pf_attn16_lds_bytes(uint32_t hd) {
+  return ((size_t)PF_ATT_KT * (hd + 8) * 2 + (size_t)hd * (PF_ATT_KT + 8) * 2) * 2;
 }

@@ -128,6 +128,7 @@ struct talos_hip_ctx {
   int32_t* pf_tok = nullptr;
   bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
   bool pf_f16 = true;       // TALOS_HIP_PF16=0: Q4_0/Q8_0 prefill GEMMs on f32 MFMA instead of split f16
+  bool pf_attn16 = true;    // TALOS_HIP_PFA16=0: prefill attention on f32 MFMA instead of split f16
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -1102,6 +1103,21 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
   A.scale = 1.0f / sqrtf((float)c->hd);
   const bool wide = c->group > 4 || c->hd > 128;  // 8 waves, else 4
   const dim3 grid(c->cfg.n_head_kv, (T + PF_ATT_Q - 1) / PF_ATT_Q), block(wide ? 512 : 256);
+  if (c->pf_f16 && c->pf_attn16 && c->hd % 32 == 0 && pf_attn16_lds_bytes(c->hd) <= c->max_lds) {
+    const size_t lds16 = pf_attn16_lds_bytes(c->hd);
+    switch (c->hd / 32) {
+#define PF_ATT16_CASE(N)                                                                          \
+  case N:                                                                                         \
+    if (wide) hipLaunchKernelGGL((k_pf_attn16<32 * N, 512>), grid, block, lds16, c->stream, A);  \
+    else hipLaunchKernelGGL((k_pf_attn16<32 * N, 256>), grid, block, lds16, c->stream, A);       \
+    break;
+      PF_ATT16_CASE(1) PF_ATT16_CASE(2) PF_ATT16_CASE(3) PF_ATT16_CASE(4) PF_ATT16_CASE(5) PF_ATT16_CASE(6)
+      PF_ATT16_CASE(7) PF_ATT16_CASE(8)
+#undef PF_ATT16_CASE
+      default: break;
+    }
+    return;
+  }
   const size_t lds = (size_t)PF_ATT_KT * (2 * c->hd + 20) * 4;
   switch (c->hd / 16) {
 #define PF_ATT_CASE(N)                                                                       \
@@ -1121,6 +1137,12 @@ void set_pf_attn_lds(int bytes) {
 #define PF_ATT_SET(N)                                        \
   set_max_lds((const void*)k_pf_attn<16 * N, 256>, bytes); \
   set_max_lds((const void*)k_pf_attn<16 * N, 512>, bytes);
+#define PF_ATT16_SET(N)                                        \
+  set_max_lds((const void*)k_pf_attn16<32 * N, 256>, bytes); \
+  set_max_lds((const void*)k_pf_attn16<32 * N, 512>, bytes);
+  PF_ATT16_SET(1) PF_ATT16_SET(2) PF_ATT16_SET(3) PF_ATT16_SET(4) PF_ATT16_SET(5) PF_ATT16_SET(6)
+  PF_ATT16_SET(7) PF_ATT16_SET(8)
+#undef PF_ATT16_SET
   PF_ATT_SET(1) PF_ATT_SET(2) PF_ATT_SET(3) PF_ATT_SET(4) PF_ATT_SET(5) PF_ATT_SET(6) PF_ATT_SET(7) PF_ATT_SET(8)
   PF_ATT_SET(9) PF_ATT_SET(10) PF_ATT_SET(11) PF_ATT_SET(12) PF_ATT_SET(13) PF_ATT_SET(14) PF_ATT_SET(15)
   PF_ATT_SET(16)
@@ -1216,6 +1238,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->allow_batch = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_PF16");
   c->pf_f16 = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_PFA16");
+  c->pf_attn16 = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
