@@ -592,22 +592,118 @@ __global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
 // k_pf_attn on v_mfma_f32_16x16x32_f16 (head_dim a multiple of 32): K, V, q
 // and the probabilities split as hi + lo halves, each product as three
 // MFMAs (hi hi, hi lo, lo hi; the lo lo term is below 2^-22 of the product),
-// f32 accumulation.  The tile's K rows are converted as they are staged,
-// K as [position][dim] and V transposed, [dim][position], so that every
-// operand fragment is one 16-byte LDS read.  S^T sub-tile u = 2 b + e (16
-// positions) takes its A rows in the order pi(i) = 32 b + 8 (i / 4) + 4 e +
-// i % 4: lane l then holds, over sub-tiles 2 b and 2 b + 1, the scores of
-// positions 32 b + 8 (l / 16) .. +7 for query l % 16 -- exactly its B
-// fragment of P^T for the 32-position P.V step b.
+// f32 accumulation.
+//
+// K and V come split already: k_pf_kv16 converts the layer's cached rows
+// [0, R) once per chunk into a shadow -- per KV head, K as [position][hd]
+// and V transposed in 64-position tiles, [tile][hd][64], hi and lo arrays,
+// rows R .. next multiple of 64 zero -- so that a tile of either is one
+// contiguous 16-byte-per-lane read, instead of every query block converting
+// every tile it reads.  V^T's positions are permuted within each
+// 32-position block: slot
+// 8 g + 4 e + r holds position 16 e + 4 g + r (g < 4, e < 2, r < 4).  S^T
+// sub-tile u (positions 16 u .. +15, natural K rows) leaves the scores of
+// positions 16 u + 4 (l / 16) + r in register r of lane l, so over sub-tiles
+// 2 b and 2 b + 1 lane l holds exactly slots 8 (l / 16) .. +7 of P^T's
+// 32-position step b -- its B fragment for the P.V MFMA, whose A fragment
+// (V^T in slot order) is one 16-byte LDS read.
+struct PfKv16 {
+  const float* kc;  // this layer's cache [ctx][kv_dim]
+  const float* vc;
+  uint16_t* kh;     // [n_head_kv][cap][hd]
+  uint16_t* kl;
+  uint16_t* vh;     // [n_head_kv][cap / 64][hd][64]
+  uint16_t* vl;
+  uint32_t R, kv_dim, hd, cap;
+};
+
+__device__ __forceinline__ void pf16_split(float v, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)v;
+  lo = (_Float16)(v - (float)hi);
+}
+
+__device__ __forceinline__ uint32_t pf16_bits(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// Block: 64 positions x 64 channels of K and V (grid: kv_dim / 64 rounded
+// up, cap-rounded rows / 64).
+__global__ __launch_bounds__(256) void k_pf_kv16(PfKv16 P) {
+  __shared__ float Vt[64][65];  // [position][channel]
+  const int tid = threadIdx.x;
+  const uint32_t c0 = blockIdx.x * 64, j0 = blockIdx.y * 64;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int e = tid + 256 * it, r = e >> 4, q = e & 15;  // row r, channels 4 q .. + 3
+    const uint32_t pos = j0 + r, ch = c0 + 4 * q;
+    f4 k{0.f, 0.f, 0.f, 0.f}, v{0.f, 0.f, 0.f, 0.f};
+    if (pos < P.R && ch < P.kv_dim) {
+      k = *reinterpret_cast<const f4*>(P.kc + (size_t)pos * P.kv_dim + ch);
+      v = *reinterpret_cast<const f4*>(P.vc + (size_t)pos * P.kv_dim + ch);
+    }
+    if (ch < P.kv_dim) {
+      const size_t at = ((size_t)(ch / P.hd) * P.cap + pos) * P.hd + ch % P.hd;
+      _Float16 h[4], l[4];
+      pf16_split(k.x, h[0], l[0]);
+      pf16_split(k.y, h[1], l[1]);
+      pf16_split(k.z, h[2], l[2]);
+      pf16_split(k.w, h[3], l[3]);
+      *reinterpret_cast<uint2*>(P.kh + at) = uint2{pf16_bits(h[0], h[1]), pf16_bits(h[2], h[3])};
+      *reinterpret_cast<uint2*>(P.kl + at) = uint2{pf16_bits(l[0], l[1]), pf16_bits(l[2], l[3])};
+    }
+    Vt[r][4 * q] = v.x;
+    Vt[r][4 * q + 1] = v.y;
+    Vt[r][4 * q + 2] = v.z;
+    Vt[r][4 * q + 3] = v.w;
+  }
+  __syncthreads();
+  // V^T: channel tid / 4, slots 16 (tid % 4) .. + 15 of the 64-position tile
+  const int cc = tid >> 2, piece = tid & 3;
+  if (c0 + cc >= P.kv_dim) return;
+  uint32_t hw[8], lw[8];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    _Float16 h[2], l[2];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const int k = 16 * piece + i + w;                                       // slot
+      const int p = (k & 32) | (16 * ((k >> 2) & 1) + 4 * ((k >> 3) & 3) + (k & 3));  // its position
+      pf16_split(Vt[p][cc], h[w], l[w]);
+    }
+    hw[i / 2] = pf16_bits(h[0], h[1]);
+    lw[i / 2] = pf16_bits(l[0], l[1]);
+  }
+  const uint32_t ch = c0 + cc;
+  const size_t at = (((size_t)(ch / P.hd) * (P.cap / 64) + j0 / 64) * P.hd + ch % P.hd) * 64 + 16 * piece;
+  uint4* dh = reinterpret_cast<uint4*>(P.vh + at);
+  uint4* dl = reinterpret_cast<uint4*>(P.vl + at);
+  dh[0] = uint4{hw[0], hw[1], hw[2], hw[3]};
+  dh[1] = uint4{hw[4], hw[5], hw[6], hw[7]};
+  dl[0] = uint4{lw[0], lw[1], lw[2], lw[3]};
+  dl[1] = uint4{lw[4], lw[5], lw[6], lw[7]};
+}
+
+struct PfAttn16 {
+  const float* Q;      // [T][n] (rotated)
+  const uint16_t* kh;  // k_pf_kv16's shadow of this layer's rows
+  const uint16_t* kl;
+  const uint16_t* vh;
+  const uint16_t* vl;
+  float* out;          // [T][n]
+  uint32_t T, p0, n, group, cap;
+  float scale;         // 1 / sqrt(hd)
+};
+
+// NT threads (one wave per q head of the group, 4 or 8 waves); the K and V
+// tile for positions j0 .. j0 + 63 (hi and lo) is fetched as 16-byte pieces
+// into registers one tile ahead of the tile being computed, then written to
+// LDS between two block syncs.
 template <int HD, int NT>
-__global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn A) {
-  static_assert(HD % 32 == 0, "head_dim a multiple of 32");
-  constexpr int KP = HD + 8;                  // K halves pitch
-  constexpr int VP = PF_ATT_KT + 8;           // transposed V halves pitch
-  constexpr int F4 = PF_ATT_KT * HD / 4;      // K float4 per tile
-  constexpr int CK = (F4 + NT - 1) / NT;      // ... per thread
-  constexpr int VQ = PF_ATT_KT / 2 * HD / 4;  // V (position pair, dim quad) per tile
-  constexpr int CV = (VQ + NT - 1) / NT;
+__global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn16 A) {
+  static_assert(HD % 32 == 0 && (16 * HD) % NT == 0, "head_dim a multiple of 32");
+  constexpr int KP = HD + 8;          // K halves pitch (conflict-free row reads)
+  constexpr int VP = PF_ATT_KT + 8;   // V^T halves pitch
+  constexpr int PC = 16 * HD / NT;    // 16-byte pieces per thread, each of K and V
   extern __shared__ float sm[];
   _Float16* Kh = reinterpret_cast<_Float16*>(sm);
   _Float16* Kl = Kh + PF_ATT_KT * KP;
@@ -644,69 +740,38 @@ __global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn A) {
 #pragma unroll
   for (int i = 0; i < HD / 16; ++i) o[i] = pf4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
+  const int first = (int)(A.p0 + t0);  // the block's earliest query position
   const int last = (int)(A.p0 + min(t0 + PF_ATT_Q, A.T) - 1);
-  const float* kbase = A.kc + (size_t)kvh * HD;
-  const float* vbase = A.vc + (size_t)kvh * HD;
-  f4 kr[CK], vr[CV][2];
-  // K float4 e: position e / (HD / 4), dims 4 (e % (HD / 4)) .. +3; V item e:
-  // positions 2 (e / (HD / 4)) and + 1, the same dims.  Rows past `last` (and
-  // items past the tile) read a clamped row and are zeroed when stored.
+  u4 kr[PC], vr[PC];
+  // K piece e: array e / (8 HD) (hi, lo), position (e / (HD / 8)) % 64,
+  // channels 8 (e % (HD / 8)) .. +7; V piece e: array e / (8 HD), channel
+  // (e / 8) % HD, slots 8 (e % 8) .. +7.
   auto fetch = [&](int j0) {
 #pragma unroll
-    for (int c = 0; c < CK; ++c) {
-      const int e = tid + NT * c, pj = min(e / (HD / 4), PF_ATT_KT - 1), d4 = e % (HD / 4);
-      kr[c] = *reinterpret_cast<const f4*>(kbase + (size_t)min(j0 + pj, last) * A.kv_dim + 4 * d4);
-    }
-#pragma unroll
-    for (int c = 0; c < CV; ++c) {
-      const int e = tid + NT * c, pp = min(e / (HD / 4), PF_ATT_KT / 2 - 1), d4 = e % (HD / 4);
-#pragma unroll
-      for (int w = 0; w < 2; ++w)
-        vr[c][w] = *reinterpret_cast<const f4*>(vbase + (size_t)min(j0 + 2 * pp + w, last) * A.kv_dim + 4 * d4);
+    for (int c = 0; c < PC; ++c) {
+      const int e = tid + NT * c, hl = e / (8 * HD), r = e % (8 * HD);
+      const int pj = r / (HD / 8), ck = r % (HD / 8);
+      const uint16_t* src = hl ? A.kl : A.kh;
+      kr[c] = *reinterpret_cast<const u4*>(src + ((size_t)kvh * A.cap + j0 + pj) * HD + 8 * ck);
+      const int d = r / 8, cv = r % 8;
+      const uint16_t* vsrc = hl ? A.vl : A.vh;
+      vr[c] = *reinterpret_cast<const u4*>(vsrc + (((size_t)kvh * (A.cap / 64) + j0 / 64) * HD + d) * 64 + 8 * cv);
     }
   };
-  auto split2 = [](float a, float b, uint32_t& hi, uint32_t& lo) {
-    const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-    const _Float16 al = (_Float16)(a - (float)ah), bl = (_Float16)(b - (float)bh);
-    hi = (uint32_t)__builtin_bit_cast(uint16_t, ah) | ((uint32_t)__builtin_bit_cast(uint16_t, bh) << 16);
-    lo = (uint32_t)__builtin_bit_cast(uint16_t, al) | ((uint32_t)__builtin_bit_cast(uint16_t, bl) << 16);
-  };
-  auto put = [&](int j0) {
+  auto put = [&]() {
 #pragma unroll
-    for (int c = 0; c < CK; ++c) {
-      const int e = tid + NT * c, pj = e / (HD / 4), d4 = e % (HD / 4);
-      if (e < F4) {
-        const f4 z{0.f, 0.f, 0.f, 0.f};
-        const f4 v = j0 + pj <= last ? kr[c] : z;
-        uint2 hi, lo;
-        split2(v.x, v.y, hi.x, lo.x);
-        split2(v.z, v.w, hi.y, lo.y);
-        *reinterpret_cast<uint2*>(Kh + pj * KP + 4 * d4) = hi;
-        *reinterpret_cast<uint2*>(Kl + pj * KP + 4 * d4) = lo;
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < CV; ++c) {
-      const int e = tid + NT * c, pp = e / (HD / 4), d4 = e % (HD / 4);
-      if (e < VQ) {
-        const f4 z{0.f, 0.f, 0.f, 0.f};
-        const f4 a = j0 + 2 * pp <= last ? vr[c][0] : z;
-        const f4 b = j0 + 2 * pp + 1 <= last ? vr[c][1] : z;
-        const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint32_t hi, lo;
-          split2(av[k], bv[k], hi, lo);
-          *reinterpret_cast<uint32_t*>(Vh + (4 * d4 + k) * VP + 2 * pp) = hi;
-          *reinterpret_cast<uint32_t*>(Vl + (4 * d4 + k) * VP + 2 * pp) = lo;
-        }
-      }
+    for (int c = 0; c < PC; ++c) {
+      const int e = tid + NT * c, hl = e / (8 * HD), r = e % (8 * HD);
+      const int pj = r / (HD / 8), ck = r % (HD / 8);
+      *reinterpret_cast<u4*>((hl ? Kl : Kh) + pj * KP + 8 * ck) = kr[c];
+      const int d = r / 8, cv = r % 8;
+      *reinterpret_cast<u4*>((hl ? Vl : Vh) + d * VP + 8 * cv) = vr[c];
     }
   };
   fetch(0);
   for (int j0 = 0; j0 <= last; j0 += PF_ATT_KT) {
     __syncthreads();
-    put(j0);
+    put();
     __syncthreads();
     fetch(j0 + PF_ATT_KT <= last ? j0 + PF_ATT_KT : j0);
     if (!live) continue;
@@ -714,37 +779,42 @@ __global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn A) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       st[u] = pf4{0.f, 0.f, 0.f, 0.f};
-      const int p = 32 * (u >> 1) + 8 * (li >> 2) + 4 * (u & 1) + (li & 3);  // pi(li) of sub-tile u
 #pragma unroll
       for (int s = 0; s < HD / 32; ++s) {
-        const pfh8 kh = *reinterpret_cast<const pfh8*>(Kh + p * KP + 32 * s + 8 * g);
-        const pfh8 kl = *reinterpret_cast<const pfh8*>(Kl + p * KP + 32 * s + 8 * g);
+        const pfh8 kh = *reinterpret_cast<const pfh8*>(Kh + (16 * u + li) * KP + 32 * s + 8 * g);
+        const pfh8 kl = *reinterpret_cast<const pfh8*>(Kl + (16 * u + li) * KP + 32 * s + 8 * g);
         st[u] = mfma16x32h(kh, qh[s], st[u]);
         st[u] = mfma16x32h(kh, ql[s], st[u]);
         st[u] = mfma16x32h(kl, qh[s], st[u]);
       }
     }
-    // register r of sub-tile u: position j0 + 32 (u / 2) + 8 g + 4 (u % 2) + r
-    float mx = -INFINITY;
+    // register r of sub-tile u: position j0 + 16 u + 4 g + r; only a tile
+    // reaching past the block's earliest query holds positions to mask
+    if (j0 + PF_ATT_KT - 1 > first) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (j0 + 16 * u + 4 * g + r > qpos) st[u][r] = -INFINITY;
+    }
+    // Position 0 is in every query's first tile, so m is finite from then on
+    // and exp2 of a masked score is 0.
+    float mx = st[0][0];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = j0 + 32 * (u >> 1) + 8 * g + 4 * (u & 1) + r;
-        if (j > qpos) st[u][r] = -INFINITY;
-        mx = fmaxf(mx, st[u][r]);
-      }
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[u][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mn = fmaxf(m, mx);
-    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
     m = mn;
     float ps = 0.f;
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = st[u][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[u][r] - mn);
+        const float pv = __builtin_amdgcn_exp2f(st[u][r] - mn);
         st[u][r] = pv;
         ps += pv;
       }
@@ -759,9 +829,10 @@ __global__ __launch_bounds__(NT) void k_pf_attn16(PfAttn A) {
       pfh8 ph, pl;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float v = st[2 * b + (i >> 2)][i & 3];
-        ph[i] = (_Float16)v;
-        pl[i] = (_Float16)(v - (float)ph[i]);
+        _Float16 hi, lo;
+        pf16_split(st[2 * b + (i >> 2)][i & 3], hi, lo);
+        ph[i] = hi;
+        pl[i] = lo;
       }
 #pragma unroll
       for (int i = 0; i < HD / 16; ++i) {

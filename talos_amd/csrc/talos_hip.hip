@@ -125,6 +125,11 @@ struct talos_hip_ctx {
   uint32_t pf_cap = 0;
   float *pf_x = nullptr, *pf_xn = nullptr, *pf_qr = nullptr, *pf_q = nullptr, *pf_att = nullptr;
   float *pf_kr = nullptr, *pf_vr = nullptr, *pf_g = nullptr, *pf_u = nullptr, *pf_h = nullptr;
+  // split-f16 shadow of one layer's K/V rows for k_pf_attn16 (k_pf_kv16):
+  // per KV head K [kv_cap][hd] and V^T in 64-position tiles, hi and lo;
+  // kv_cap = the context length rounded up to 64
+  uint16_t *pf_kh = nullptr, *pf_kl = nullptr, *pf_vh = nullptr, *pf_vl = nullptr;
+  uint32_t pf_kv_cap = 0;
   int32_t* pf_tok = nullptr;
   bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
   bool pf_f16 = true;       // TALOS_HIP_PF16=0: Q4_0/Q8_0 prefill GEMMs on f32 MFMA instead of split f16
@@ -1026,7 +1031,19 @@ int pf_supported(talos_hip_ctx* c, bool* ok) {
   return TALOS_OK;
 }
 
+// The prefill attention runs on f16 matrix cores with split operands when
+// head_dim is a multiple of 32 and its tiles fit the LDS.
+bool pf_attn16_on(const talos_hip_ctx* c) {
+  return c->pf_f16 && c->pf_attn16 && c->hd % 32 == 0 && pf_attn16_lds_bytes(c->hd) <= c->max_lds;
+}
+
 int pf_reserve(talos_hip_ctx* c, uint32_t T) {
+  if (pf_attn16_on(c) && !c->pf_kh) {
+    const uint32_t cap = (c->cfg.context_length + 63) / 64 * 64;
+    const size_t bytes = (size_t)cap * c->kv_dim * 2;
+    for (uint16_t** p : {&c->pf_kh, &c->pf_kl, &c->pf_vh, &c->pf_vl}) HIPCHK(c, hipMalloc(p, bytes));
+    c->pf_kv_cap = cap;
+  }
   if (c->pf_cap >= T) return TALOS_OK;
   (void)hipStreamSynchronize(c->stream);
   for (float** p : {&c->pf_x, &c->pf_xn, &c->pf_qr, &c->pf_q, &c->pf_att, &c->pf_kr, &c->pf_vr, &c->pf_g, &c->pf_u,
@@ -1103,13 +1120,40 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
   A.scale = 1.0f / sqrtf((float)c->hd);
   const bool wide = c->group > 4 || c->hd > 128;  // 8 waves, else 4
   const dim3 grid(c->cfg.n_head_kv, (T + PF_ATT_Q - 1) / PF_ATT_Q), block(wide ? 512 : 256);
-  if (c->pf_f16 && c->pf_attn16 && c->hd % 32 == 0 && pf_attn16_lds_bytes(c->hd) <= c->max_lds) {
+  if (pf_attn16_on(c)) {
+    // the layer's rows [0, p0 + T) split into the shadow (rows up to the
+    // next multiple of 64 zero), then the attention over it
+    PfKv16 P{};
+    P.kc = c->kc[l];
+    P.vc = c->vc[l];
+    P.kh = c->pf_kh;
+    P.kl = c->pf_kl;
+    P.vh = c->pf_vh;
+    P.vl = c->pf_vl;
+    P.R = p0 + T;
+    P.kv_dim = c->kv_dim;
+    P.hd = c->hd;
+    P.cap = c->pf_kv_cap;
+    hipLaunchKernelGGL(k_pf_kv16, dim3((c->kv_dim + 63) / 64, (P.R + 63) / 64), dim3(256), 0, c->stream, P);
+    PfAttn16 B{};
+    B.Q = c->pf_q;
+    B.kh = c->pf_kh;
+    B.kl = c->pf_kl;
+    B.vh = c->pf_vh;
+    B.vl = c->pf_vl;
+    B.out = c->pf_att;
+    B.T = T;
+    B.p0 = p0;
+    B.n = c->cfg.n_embd;
+    B.group = c->group;
+    B.cap = c->pf_kv_cap;
+    B.scale = A.scale;
     const size_t lds16 = pf_attn16_lds_bytes(c->hd);
     switch (c->hd / 32) {
 #define PF_ATT16_CASE(N)                                                                          \
   case N:                                                                                         \
-    if (wide) hipLaunchKernelGGL((k_pf_attn16<32 * N, 512>), grid, block, lds16, c->stream, A);  \
-    else hipLaunchKernelGGL((k_pf_attn16<32 * N, 256>), grid, block, lds16, c->stream, A);       \
+    if (wide) hipLaunchKernelGGL((k_pf_attn16<32 * N, 512>), grid, block, lds16, c->stream, B);  \
+    else hipLaunchKernelGGL((k_pf_attn16<32 * N, 256>), grid, block, lds16, c->stream, B);       \
     break;
       PF_ATT16_CASE(1) PF_ATT16_CASE(2) PF_ATT16_CASE(3) PF_ATT16_CASE(4) PF_ATT16_CASE(5) PF_ATT16_CASE(6)
       PF_ATT16_CASE(7) PF_ATT16_CASE(8)
@@ -1315,6 +1359,7 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
                  c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out, c->samp_u, c->nll, c->pf_x, c->pf_xn,
                  c->pf_qr, c->pf_q, c->pf_att, c->pf_kr, c->pf_vr, c->pf_g, c->pf_u, c->pf_h, c->pf_tok,
+                 c->pf_kh, c->pf_kl, c->pf_vh, c->pf_vl,
                  c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart, c->qraw, c->kraw,
                  c->vraw, c->graw, c->uraw, c->scores};
   for (void* p : dev)
