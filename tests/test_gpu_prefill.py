@@ -78,3 +78,44 @@ def test_multi_chunk_prefill_and_continuation(talos, oracle, monkeypatch):
     assert am2 == am and float(np.abs(lg2 - lg).max()) <= 1e-3
     assert list(m2.decode_greedy(am2, n, 16)) == list(cont)
     m2.close()
+
+
+@pytest.mark.parametrize("pfa16", [None, "0"], ids=["attn_f16", "attn_f32"])
+def test_prefill_after_decode_wide_group(talos, oracle, monkeypatch, pfa16):
+    """A prompt, greedy decode steps, then a second prompt at the next
+    position, on a Q8_0 model with 8 q heads per KV head (head_dim 64: the
+    attention's 8-wave blocks): the second prefill attends over rows the
+    decode steps wrote, which the split-f16 attention reads through its
+    shadow of the cache.  Last logits and every cache row against the
+    oracle's token loop over the same sequence; TALOS_HIP_PFA16=0 runs the
+    f32-MFMA attention on the same case."""
+    from talos_amd import SynthSpec, GGML_F32, GGML_Q8_0
+    if pfa16 is not None:
+        monkeypatch.setenv("TALOS_HIP_PFA16", pfa16)
+    spec = SynthSpec(n_layer=2, n_head=16, n_head_kv=2, n_embd=1024, n_ff=1024, vocab_size=512,
+                     context_length=256, layer_type=GGML_Q8_0, output_type=GGML_Q8_0, embd_type=GGML_F32,
+                     seed=61, name="group8_q8")
+    rng = np.random.default_rng(62)
+    p1 = [int(t) for t in rng.integers(0, spec.vocab_size, 40)]
+    p2 = [int(t) for t in rng.integers(0, spec.vocab_size, 70)]
+    _step(f"group-8 Q8_0: 40-token prompt, 12 greedy steps, 70-token prompt at 52 (PFA16={pfa16})")
+    m = talos.Model.synth(spec)
+    _, am = m.prefill(p1, 0)
+    toks = [int(t) for t in m.decode_greedy(am, len(p1), 12)]
+    fed = p1 + [int(am)] + toks[:11]
+    lg, am2 = m.prefill(p2, len(fed))
+    seq = fed + p2
+    kg, vg = m.kv_read(len(seq))
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=16)
+    for p, t in enumerate(seq):
+        c = ref.forward(t, p)
+    kc, vc = ref.get_kv(len(seq))
+    d = float(np.abs(lg - c).max())
+    dk = float(max(np.abs(kg - kc).max(), np.abs(vg - vc).max()))
+    print(f"  last logits max abs {d:.3e}, K/V max abs {dk:.3e}; argmax gpu {am2} cpu {oracle.argmax(c)}",
+          flush=True)
+    assert d <= 1e-3 and dk <= 1e-3 and am2 == oracle.argmax(c)
+    record_parity(f"group8_q8_prefill_after_decode_{'f32attn' if pfa16 else 'f16attn'}", max(d, dk), 1e-3,
+                  path="batched_prefill")
+    ref.close()
+    m.close()
