@@ -185,11 +185,11 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(PfGemm G) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   // this block's matrix and row tile
-  uint32_t tile = blockIdx.x, s = 0;
+  uint32_t tile = blockIdx.y, s = 0;
   while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
   const PfSeg& S = G.S[s];
   const uint32_t M = S.W.rows;
-  const uint32_t tb = blockIdx.y * PF_TOK;
+  const uint32_t tb = blockIdx.x * PF_TOK;
   const uint32_t row = tile * PF_ROWS + (uint32_t)wave * 16 + li;
   const uint32_t rowc = row < M ? row : M - 1;
   pf4 acc[4];
@@ -356,11 +356,11 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   __shared__ _Float16 Xs[2][2][64 * PF_HP];  // [buffer][hi, lo][token][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  uint32_t tile = blockIdx.x, s = 0;
+  uint32_t tile = blockIdx.y, s = 0;
   while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
   const PfSeg& S = G.S[s];
   const uint32_t M = S.W.rows;
-  const uint32_t tb = blockIdx.y * 64;
+  const uint32_t tb = blockIdx.x * 64;
   const uint32_t row = tile * PF_ROWS + (uint32_t)wave * 16 + li;
   const uint32_t rowc = row < M ? row : M - 1;
   pf4 acc[4];

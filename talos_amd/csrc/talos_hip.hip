@@ -1090,7 +1090,11 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float
       tiles += S.tiles;
       ++i;
     }
-    const dim3 grid(tiles, (T + PF_TOK - 1) / PF_TOK);
+    // token tiles on x: a row tile's token tiles go out together and land
+    // on the XCDs round-robin by token tile, so each XCD's L2 serves a few
+    // token tiles of X and a row tile's weights are fetched about once per
+    // XCD (+0.6 % at a 16k prompt against row tiles on x)
+    const dim3 grid((T + PF_TOK - 1) / PF_TOK, tiles);
     switch (type) {
       case TALOS_GGML_Q4_0:
         if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
