@@ -117,8 +117,8 @@ int talos_hip_decode_greedy(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, ui
 /* Prompt processing on the device: run tokens[0..n) at positions
  * pos..pos+n-1 (the prefill loop of src/main.rs:88-94, Model::step per
  * prompt token) and leave the cache and the device state as that loop does.
- * Models whose layer matrices are F32, Q4_0 or Q8_0 with head_dim a
- * multiple of 16 up to 256 (n_head * head_dim == n_embd, groups up to 8)
+ * Models with head_dim a multiple of 16 up to 256 (n_head * head_dim ==
+ * n_embd, groups up to 8), whatever their layer matrices' formats,
  * take the prompt in chunks of up to 1024 tokens through each layer at once
  * on the matrix cores: the same products and f32 sums in another order, so
  * within f32 rounding of the token loop rather than bit-identical.  Other

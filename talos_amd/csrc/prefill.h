@@ -87,6 +87,16 @@ template <>
 struct PfW<TALOS_FMT_F32> {
   float v[2][8];
 };
+// Q6_K: a 64-wide K chunk is two quarters (32-element runs) of one half
+// super-block, held by the two 16-byte layout chunks g2 = 0, 1 of that half
+// (elements 16 g2 .. +15 of each quarter): their low-nibble planes a, b, the
+// high-bit plane h and the four int8 sub-scales, and the super-block's d.
+template <>
+struct PfW<TALOS_FMT_Q6_K> {
+  u4 a[2], b[2], h[2];
+  uint32_t sc[2];
+  float d;
+};
 
 template <uint32_t FMT>
 __device__ __forceinline__ void pf_load_w(PfW<FMT>& F, const DevMat& W, uint32_t rowc, uint32_t k0, uint32_t K,
@@ -100,6 +110,19 @@ __device__ __forceinline__ void pf_load_w(PfW<FMT>& F, const DevMat& W, uint32_t
         const uint32_t k = k0 + 32 * blk + 4 * s + g;
         F.v[blk][s] = wr[k < K ? k : K - 1];
       }
+  } else if constexpr (FMT == TALOS_FMT_Q6_K) {
+    // K % 256 == 0, so k0 < K is inside the row
+    const uint32_t nc = W.nchunk, sb = k0 / 256, c0 = sb * 4 + ((k0 % 256) / 128) * 2;
+    const uint8_t* base = W.q + (size_t)rowc * nc * 48;
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const size_t c = c0 + g2;
+      F.a[g2] = *reinterpret_cast<const u4*>(base + c * 16);
+      F.b[g2] = *reinterpret_cast<const u4*>(base + (size_t)nc * 16 + c * 16);
+      F.h[g2] = *reinterpret_cast<const u4*>(base + (size_t)nc * 32 + c * 16);
+      F.sc[g2] = W.sc[(size_t)rowc * nc + c];
+    }
+    F.d = f16_to_f32(W.d[(size_t)rowc * (nc / 4) + sb]);
   } else {
     const uint32_t nb = K / 32;
     uint32_t dd[2];
@@ -127,6 +150,21 @@ __device__ __forceinline__ void pf_dequant(const PfW<FMT>& F, int blk, uint32_t 
   if constexpr (FMT == TALOS_FMT_F32) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) b[s] = kb + 4 * s + g < K ? F.v[blk][s] : 0.f;
+  } else if constexpr (FMT == TALOS_FMT_Q6_K) {
+    // element j = 4 s + g of quarter qt (src/gguf/dtype.rs:98-118): byte
+    // j % 16 of layout chunk j / 16 -- the low nibble of plane a (quarter 0)
+    // or b (1), the high nibble of a (2) or b (3), and bits 2 qt, 2 qt + 1
+    // of plane h above it; y = d * sub-scale * (q - 32)
+    const uint32_t qt = (kb % 128) / 32;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int g2 = s >> 2, w = s & 3;  // j / 16, (j % 16) / 4
+      const uint32_t lw = (qt & 1) ? F.b[g2][w] : F.a[g2][w];
+      const uint32_t by = (lw >> (8 * g)) & 0xFFu, hb = (F.h[g2][w] >> (8 * g + 2 * qt)) & 3u;
+      const int q = (int)((qt < 2 ? by & 0x0Fu : by >> 4) | (hb << 4)) - 32;
+      const float sub = (float)(int8_t)((F.sc[g2] >> (8 * qt)) & 0xFFu);
+      b[s] = F.d * sub * (float)q;
+    }
   } else {
     const float d = f16_to_f32((uint16_t)(F.d >> (16 * blk)));
     if constexpr (FMT == TALOS_FMT_Q4_0) {

@@ -1011,9 +1011,9 @@ void enq_sample(talos_hip_ctx* c, const float* logits, uint32_t n, float tempera
 
 #define PF_CHUNK 1024
 
-// The batched path takes layers whose matrices are F32, Q4_0 or Q8_0 and
-// attention heads of a multiple of 16 up to 256 that tile n_embd exactly,
-// with groups of at most 8.
+// The batched path takes layer matrices of every format (F32, Q4_0, Q8_0,
+// Q6_K) and attention heads of a multiple of 16 up to 256 that tile n_embd
+// exactly, with groups of at most 8.
 int pf_supported(talos_hip_ctx* c, bool* ok) {
   *ok = false;
   if (!c->allow_batch || c->hd % 16 || c->hd > 256 || c->group > 8 || c->cfg.n_embd != c->cfg.n_head * c->hd ||
@@ -1023,8 +1023,6 @@ int pf_supported(talos_hip_ctx* c, bool* ok) {
     LayerW w;
     int rc = layer_weights(c, l, &w);
     if (rc) return rc;
-    for (const DevWeight* m : {w.q, w.k, w.v, w.o, w.g, w.u, w.d})
-      if (m->type == TALOS_GGML_Q6_K) return TALOS_OK;
   }
   const size_t lds = (size_t)PF_ATT_KT * (2 * c->hd + 20) * 4;
   *ok = lds <= c->max_lds;
@@ -1104,6 +1102,7 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float
         if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
         else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
         break;
+      case TALOS_GGML_Q6_K: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q6_K>, grid, dim3(PF_NT), 0, c->stream, G); break;
       default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(PF_NT), 0, c->stream, G); break;
     }
   }

@@ -8,6 +8,7 @@ that continues from either kind of prefill identically."""
 import numpy as np
 import pytest
 
+from tests import models as MB
 from tests.conftest import record_parity
 
 pytestmark = pytest.mark.gpu
@@ -117,5 +118,48 @@ def test_prefill_after_decode_wide_group(talos, oracle, monkeypatch, pfa16):
     assert d <= 1e-3 and dk <= 1e-3 and am2 == oracle.argmax(c)
     record_parity(f"group8_q8_prefill_after_decode_{'f32attn' if pfa16 else 'f16attn'}", max(d, dk), 1e-3,
                   path="batched_prefill")
+    ref.close()
+    m.close()
+
+
+@pytest.mark.parametrize("case", ["q6k_layers", "mixed_formats"])
+def test_prefill_q6k_and_mixed_formats(talos, oracle, case):
+    """Layer matrices in Q6_K (the f32-MFMA GEMM dequantizing Q6_K), and a
+    model whose layer tensors mix F32, Q8_0, Q4_0 and Q6_K (q/k/v and
+    gate/up then go out as one GEMM launch per format): a 100-token batched
+    prefill's last logits and every cache row against the oracle's token
+    loop."""
+    from talos_amd import SynthSpec, GGML_F32, GGML_Q6_K
+    if case == "q6k_layers":
+        spec = SynthSpec(n_layer=2, n_head=8, n_head_kv=2, n_embd=512, n_ff=1024, vocab_size=1024,
+                         context_length=256, layer_type=GGML_Q6_K, output_type=GGML_Q6_K, embd_type=GGML_F32,
+                         seed=71, name="q6k_layers")
+        m = talos.Model.synth(spec)
+        vocab = spec.vocab_size
+    else:
+        shape = dict(embd=256, n_head=4, n_head_kv=2, ff=512, vocab=300, n_layer=2)
+        W = MB.normal_model(63, **shape)
+        types = {"output.weight": 14, "token_embd.weight": 8}
+        for l in range(shape["n_layer"]):
+            p = f"blk.{l}."
+            types.update({p + "attn_q.weight": 8, p + "attn_k.weight": 2, p + "attn_v.weight": 0,
+                          p + "attn_output.weight": 2, p + "ffn_gate.weight": 8, p + "ffn_up.weight": 0,
+                          p + "ffn_down.weight": 14})
+        m = talos.Model.load_bytes(MB.gguf_bytes(W, ctx=128, types=types, **shape))
+        vocab = shape["vocab"]
+    n = 100
+    prompt = [int(t) for t in np.random.default_rng(72).integers(0, vocab, n)]
+    _step(f"{case}: {n}-token prompt")
+    lg, am = m.prefill(prompt, 0)
+    kg, vg = m.kv_read(n)
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=16)
+    for p, t in enumerate(prompt):
+        c = ref.forward(t, p)
+    kc, vc = ref.get_kv(n)
+    d = float(np.abs(lg - c).max())
+    dk = float(max(np.abs(kg - kc).max(), np.abs(vg - vc).max()))
+    print(f"  last logits max abs {d:.3e}, K/V max abs {dk:.3e}; argmax gpu {am} cpu {oracle.argmax(c)}", flush=True)
+    assert d <= 1e-3 and dk <= 1e-3 and am == oracle.argmax(c)
+    record_parity(f"{case}_batched_prefill_{n}", max(d, dk), 1e-3, path="batched_prefill")
     ref.close()
     m.close()
