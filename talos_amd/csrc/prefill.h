@@ -322,6 +322,19 @@ template <uint32_t FMT>
 __device__ __forceinline__ void pf16_load_w(PfW16& F, const DevMat& W, uint32_t rowc, uint32_t k0, uint32_t K,
                                             int g) {
   const uint32_t nb = K / 32;
+  if (FMT == TALOS_FMT_Q8_0 && nb % 2 == 0) {
+    // the chunk's 64 quant bytes (blocks k0 / 32 and + 1, contiguous) as four
+    // 16-byte pieces, piece g in lane group g; pf16_swap_q8 then gives every
+    // lane 8 bytes of each block
+    const size_t ci = (size_t)rowc * nb + k0 / 32;
+    const u4 v = *reinterpret_cast<const u4*>(W.q + ci * 32 + 16 * g);
+    F.q[0][0] = v.x;
+    F.q[0][1] = v.y;
+    F.q[1][0] = v.z;
+    F.q[1][1] = v.w;
+    F.d = *reinterpret_cast<const uint32_t*>(W.d + ci);
+    return;
+  }
   uint32_t dd[2];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -341,6 +354,23 @@ __device__ __forceinline__ void pf16_load_w(PfW16& F, const DevMat& W, uint32_t 
   // 14 % off the 1024-token gate/up GEMM)
   F.d = nb % 2 ? dd[0] | (dd[1] << 16) : *reinterpret_cast<const uint32_t*>(W.d + (size_t)rowc * nb + k0 / 32);
 }
+// After the one-load fetch of a Q8_0 chunk, lane group g holds bytes
+// 16 g .. +15 of the chunk (groups 0, 1: block 0; groups 2, 3: block 1).
+// v_permlane32_swap trades the upper 32 lanes of its first operand for the
+// lower 32 of its second, so swapping words 0, 1 (upper half: groups 2, 3)
+// with words 2, 3 (lower half: groups 0, 1) leaves words 0, 1 of every lane
+// on block 0 and words 2, 3 on block 1: group g then holds bytes 8 s(g) ..
+// +7 of each block, s = (0, 2, 1, 3), the k order its X fragments are read
+// in.
+__device__ __forceinline__ void pf16_swap_q8(PfW16& F) {
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(F.q[0][w], F.q[1][w], false, false);
+    F.q[0][w] = r[0];
+    F.q[1][w] = r[1];
+  }
+}
+
 // The 8 weights of block blk as f16 integers (zero past K): each byte b
 // (a Q8_0 q + 128, or a Q4_0 nibble) becomes the half 1024 + b by placing
 // 0x64 above it, then the offset is subtracted (exact in f16).
@@ -410,6 +440,11 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = pf4{0.f, 0.f, 0.f, 0.f};
   const int nchunks = (int)((G.K + PF_KC - 1) / PF_KC);
+  // Q8_0 rows of an even block count take the one-load fetch: lane group g
+  // then holds elements 8 s(g) .. +7 of each block (pf16_swap_q8), and its X
+  // fragments are read in that k order
+  const bool q8one = FMT == TALOS_FMT_Q8_0 && (G.K / 32) % 2 == 0;
+  const int kg = q8one ? ((g & 1) << 1) | (g >> 1) : g;
   PfW16 wc, wn;
   PfX16 xc, xn;
   pf16_load_w<FMT>(wc, S.W, rowc, 0, G.K, g);
@@ -422,6 +457,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
     const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
     pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
     pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
+    if (q8one) pf16_swap_q8(wc);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       const bool live = k0 + 32 * blk < G.K;
@@ -429,7 +465,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
       const float d = f16_to_f32((uint16_t)(wc.d >> (16 * blk)));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int off = (16 * t + li) * PF_HP + 32 * blk + 8 * g;
+        const int off = (16 * t + li) * PF_HP + 32 * blk + 8 * kg;
         const pfh8 ah = *reinterpret_cast<const pfh8*>(Xh + off);
         const pfh8 al = *reinterpret_cast<const pfh8*>(Xl + off);
         pf4 blkacc = mfma16x32h(ah, b, pf4{0.f, 0.f, 0.f, 0.f});
