@@ -335,6 +335,17 @@ __device__ __forceinline__ void pf16_load_w(PfW16& F, const DevMat& W, uint32_t 
     F.d = *reinterpret_cast<const uint32_t*>(W.d + ci);
     return;
   }
+  if (FMT == TALOS_FMT_Q4_0 && nb % 2 == 0) {
+    // the chunk's 32 quant bytes as four 8-byte pieces, piece g in lane
+    // group g (groups 0, 1: block 0; groups 2, 3: block 1); pf16_swap_q4
+    // then gives every lane 8 bytes of each block
+    const size_t ci = (size_t)rowc * nb + k0 / 32;
+    const uint2 v = *reinterpret_cast<const uint2*>(W.q + ci * 16 + 8 * g);
+    F.q[0][0] = v.x;
+    F.q[0][1] = v.y;
+    F.d = *reinterpret_cast<const uint32_t*>(W.d + ci);
+    return;
+  }
   uint32_t dd[2];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -366,6 +377,21 @@ __device__ __forceinline__ void pf16_swap_q8(PfW16& F) {
 #pragma unroll
   for (int w = 0; w < 2; ++w) {
     const auto r = __builtin_amdgcn_permlane32_swap(F.q[0][w], F.q[1][w], false, false);
+    F.q[0][w] = r[0];
+    F.q[1][w] = r[1];
+  }
+}
+
+// After the one-load fetch of a Q4_0 chunk, lane group g holds bytes 8 g ..
+// +7 of the chunk.  Swapping a word with itself copies the lower 32 lanes'
+// value into the upper ones (first result) and the upper lanes' into the
+// lower (second): every lane then holds bytes 8 (g & 1) .. +7 of block 0 and
+// of block 1 -- exactly what the direct two-load fetch gives it (groups 0, 1
+// take the low nibbles, 2, 3 the high).
+__device__ __forceinline__ void pf16_swap_q4(PfW16& F) {
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const auto r = __builtin_amdgcn_permlane32_swap(F.q[0][w], F.q[0][w], false, false);
     F.q[0][w] = r[0];
     F.q[1][w] = r[1];
   }
@@ -443,7 +469,8 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   // Q8_0 rows of an even block count take the one-load fetch: lane group g
   // then holds elements 8 s(g) .. +7 of each block (pf16_swap_q8), and its X
   // fragments are read in that k order
-  const bool q8one = FMT == TALOS_FMT_Q8_0 && (G.K / 32) % 2 == 0;
+  const bool one = (G.K / 32) % 2 == 0;  // the one-load fetch (Q8_0 and Q4_0)
+  const bool q8one = FMT == TALOS_FMT_Q8_0 && one;
   const int kg = q8one ? ((g & 1) << 1) | (g >> 1) : g;
   PfW16 wc, wn;
   PfX16 xc, xn;
@@ -458,6 +485,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
     pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
     pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
     if (q8one) pf16_swap_q8(wc);
+    if (FMT == TALOS_FMT_Q4_0 && one) pf16_swap_q4(wc);
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       const bool live = k0 + 32 * blk < G.K;
