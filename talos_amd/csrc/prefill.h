@@ -479,11 +479,13 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   for (int c = 0; c < nchunks; ++c) {
     _Float16* Xh = Xs[c & 1][0];
     _Float16* Xl = Xs[c & 1][1];
+    const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
+    // the next chunk's X loads go out before this chunk's X is staged (the
+    // staging waits for the older loads only), its weights after the sync
+    pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
     pf16_store_x(xc, Xh, Xl, tid);
     __syncthreads();
-    const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
     pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
-    pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
     if (q8one) pf16_swap_q8(wc);
     if (FMT == TALOS_FMT_Q4_0 && one) pf16_swap_q4(wc);
 #pragma unroll
