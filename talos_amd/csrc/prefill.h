@@ -21,6 +21,25 @@
 
 typedef float pf4 __attribute__((ext_vector_type(4)));
 
+// The split-f16 GEMM's X: per row, groups of 8 elements as 8 hi halves then
+// 8 lo halves (hi = f16(x), lo = f16(x - hi)); element k of row t has its hi
+// at ((t K + (k & ~7)) * 2 + (k & 7)) and its lo 8 halves later.  The empty
+// asm statement pins x as the rounded f32 value its producer computed:
+// otherwise the compiler may fold a product feeding the conversion into
+// v_fma_mixlo_f16 (the exact product rounded once to f16) for the hi that lo
+// is computed from while converting the rounded f32 value for the hi it
+// stores, and where the two roundings differ (an f32 value on an f16
+// rounding midpoint) hi + lo is off by an f16 ulp.
+__device__ __forceinline__ void pf16_split_bits(float v, uint16_t& hi, uint16_t& lo) {
+  asm volatile("" : "+v"(v));
+  const _Float16 h = (_Float16)v;
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
+}
+__device__ __forceinline__ size_t pf16_x_at(size_t row_start, uint32_t k) {
+  return (row_start + (k & ~7u)) * 2 + (k & 7u);
+}
+
 __device__ __forceinline__ pf4 mfma16x4(float a, float b, pf4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -32,16 +51,25 @@ __global__ __launch_bounds__(256) void k_pf_embed(DevMat M, const int32_t* __res
   for (uint32_t e = threadIdx.x; e < n; e += 256) X[(size_t)t * n + e] = dq_elem(M, tok, e);
 }
 
-// Xn_t = rmsnorm(x_t) * w (src/math/ops.rs:5-12), one row per block.
+// Xn_t = rmsnorm(x_t) * w (src/math/ops.rs:5-12), one row per block; with
+// X16 also in the split-f16 GEMM's interleaved halves.
 __global__ __launch_bounds__(256) void k_pf_rmsnorm(const float* __restrict__ X, const float* __restrict__ w,
-                                                    float eps, uint32_t n, float* __restrict__ Xn) {
+                                                    float eps, uint32_t n, float* __restrict__ Xn,
+                                                    uint16_t* __restrict__ X16) {
   __shared__ float red[8];
   const float* x = X + (size_t)blockIdx.x * n;
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < n; i += 256) ss += x[i] * x[i];
   ss = block_sum(ss, red, 4);
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-  for (uint32_t i = threadIdx.x; i < n; i += 256) Xn[(size_t)blockIdx.x * n + i] = x[i] * scale * w[i];
+  for (uint32_t i = threadIdx.x; i < n; i += 256) {
+    const float v = x[i] * scale * w[i];
+    Xn[(size_t)blockIdx.x * n + i] = v;
+    if (X16) {
+      const size_t at = pf16_x_at((size_t)blockIdx.x * n, i);
+      pf16_split_bits(v, X16[at], X16[at + 8]);
+    }
+  }
 }
 
 // ------------------------------------------------------------- the GEMM --
@@ -73,6 +101,7 @@ struct PfGemm {
   PfSeg S[3];
   uint32_t nseg;
   const float* X;  // [T][K], K % 4 == 0
+  const uint16_t* X16;  // X in interleaved halves (pf16_x_at; k_pf_gemm16)
   uint32_t T, K;
   int accumulate;
 };
@@ -288,8 +317,10 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm(PfGemm G) {
 // covers one quant block (K = 32): lane l supplies A[token l % 16][k = 8
 // (l / 16) .. +7] and B[k = 8 (l / 16) .. +7][row l % 16], the same k set in
 // both, and holds D[token 4 (l / 16) + r][row l % 16] in register r.
-// Tile, waves and pipelining as k_pf_gemm; X is staged in LDS as the hi and
-// lo halves, [token][k] with a pitch of 72 halves.
+// Tile, waves and pipelining as k_pf_gemm.  X arrives split: its producer
+// (rmsnorm, attention, SwiGLU) writes the hi and lo halves beside the f32
+// rows once (pf16_x_at), instead of every row tile converting it; they are
+// staged in LDS as [token][k] halves with a pitch of 72.
 typedef _Float16 pfh8 __attribute__((ext_vector_type(8)));
 typedef _Float16 pfh2 __attribute__((ext_vector_type(2)));
 #define PF_HP 72
@@ -420,33 +451,27 @@ __device__ __forceinline__ pfh8 pf16_weights(const PfW16& F, int blk, int g, boo
   return live ? r : pfh8{0, 0, 0, 0, 0, 0, 0, 0};
 }
 
-// X[tb .. +64][k0 .. +64]: thread t holds token t / 8, elements k0 + 8 (t % 8)
-// .. +7 (zero past T and K).
+// X[tb .. +64][k0 .. +64] from the interleaved halves: thread t holds token
+// t / 8, elements k0 + 8 (t % 8) .. +7 as 8 hi and 8 lo halves (zero past T
+// and K).
 struct PfX16 {
-  f4 v[2];
+  u4 h, l;
 };
-__device__ __forceinline__ void pf16_load_x(PfX16& P, const float* __restrict__ X, uint32_t T, uint32_t K,
+__device__ __forceinline__ void pf16_load_x(PfX16& P, const uint16_t* __restrict__ X16, uint32_t T, uint32_t K,
                                             uint32_t tb, uint32_t k0, int tid) {
   const uint32_t t = tb + (uint32_t)(tid >> 3), k = k0 + 8u * (uint32_t)(tid & 7);
   const uint32_t tc = t < T ? t : T - 1, kc = k < K ? k : K - 8;
-  const float* p = X + (size_t)tc * K + kc;
-  const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+  const u4* p = reinterpret_cast<const u4*>(X16 + pf16_x_at((size_t)tc * K, kc));
+  const u4 h = p[0], l = p[1];
   const bool ok = t < T && k < K;
-  const f4 z{0.f, 0.f, 0.f, 0.f};
-  P.v[0] = ok ? a : z;
-  P.v[1] = ok ? b : z;
+  const u4 z{0u, 0u, 0u, 0u};
+  P.h = ok ? h : z;
+  P.l = ok ? l : z;
 }
 __device__ __forceinline__ void pf16_store_x(const PfX16& P, _Float16* Xh, _Float16* Xl, int tid) {
   const int tt = tid >> 3, k8 = tid & 7;
-  const float x[8] = {P.v[0].x, P.v[0].y, P.v[0].z, P.v[0].w, P.v[1].x, P.v[1].y, P.v[1].z, P.v[1].w};
-  pfh8 h, l;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    h[i] = (_Float16)x[i];
-    l[i] = (_Float16)(x[i] - (float)h[i]);
-  }
-  *reinterpret_cast<pfh8*>(Xh + tt * PF_HP + 8 * k8) = h;
-  *reinterpret_cast<pfh8*>(Xl + tt * PF_HP + 8 * k8) = l;
+  *reinterpret_cast<u4*>(Xh + tt * PF_HP + 8 * k8) = P.h;
+  *reinterpret_cast<u4*>(Xl + tt * PF_HP + 8 * k8) = P.l;
 }
 
 template <uint32_t FMT>
@@ -475,14 +500,14 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   PfW16 wc, wn;
   PfX16 xc, xn;
   pf16_load_w<FMT>(wc, S.W, rowc, 0, G.K, g);
-  pf16_load_x(xc, G.X, G.T, G.K, tb, 0, tid);
+  pf16_load_x(xc, G.X16, G.T, G.K, tb, 0, tid);
   for (int c = 0; c < nchunks; ++c) {
     _Float16* Xh = Xs[c & 1][0];
     _Float16* Xl = Xs[c & 1][1];
     const uint32_t k0 = (uint32_t)c * PF_KC, kn = (uint32_t)(c + 1 < nchunks ? c + 1 : c) * PF_KC;
     // the next chunk's X loads go out before this chunk's X is staged (the
     // staging waits for the older loads only), its weights after the sync
-    pf16_load_x(xn, G.X, G.T, G.K, tb, kn, tid);
+    pf16_load_x(xn, G.X16, G.T, G.K, tb, kn, tid);
     pf16_store_x(xc, Xh, Xl, tid);
     __syncthreads();
     pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
@@ -537,11 +562,19 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(const float* __restrict__ Qr
   }
 }
 
-// h = silu(g) * u row-wise over T rows of ff (src/math/ops.rs:28-37).
+// h = silu(g) * u row-wise over T rows of ff (src/math/ops.rs:28-37); with
+// H16 (ff % 8 == 0) also in the split-f16 GEMM's interleaved halves.
 __global__ __launch_bounds__(256) void k_pf_swiglu(const float* __restrict__ Gt, const float* __restrict__ Ut,
-                                                   float* __restrict__ H, size_t count) {
+                                                   float* __restrict__ H, uint16_t* __restrict__ H16,
+                                                   size_t count) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < count) H[i] = (Gt[i] / (1.0f + expf(-Gt[i]))) * Ut[i];
+  if (i >= count) return;
+  const float v = (Gt[i] / (1.0f + expf(-Gt[i]))) * Ut[i];
+  H[i] = v;
+  if (H16) {
+    const size_t at = (i & ~(size_t)7) * 2 + (i & 7);
+    pf16_split_bits(v, H16[at], H16[at + 8]);
+  }
 }
 
 // ---------------------------------------------------- flash attention --
@@ -564,9 +597,34 @@ struct PfAttn {
   const float* kc;   // this layer's cache [ctx][kv_dim]
   const float* vc;
   float* out;        // [T][n]
+  uint16_t* out16;   // with it, out in the split-f16 GEMM's interleaved halves too (or null)
   uint32_t T, p0, n, kv_dim, hd, group;
   float scale;       // 1 / sqrt(hd)
 };
+
+// The attention's output row for one query and head: this lane's O^T
+// registers (tile i, register r: dim 16 i + 4 g + r) times inv into
+// out[row + col0 ..] and, with out16, as interleaved hi and lo halves.
+template <int HD>
+__device__ __forceinline__ void pf_attn_store(const pf4 (&o)[HD / 16], float inv, float* out, uint16_t* out16,
+                                              size_t row, uint32_t col0, int g) {
+#pragma unroll
+  for (int i = 0; i < HD / 16; ++i) {
+    const uint32_t col = col0 + 16 * i + 4 * g;
+    const f4 v{o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv};
+    *reinterpret_cast<f4*>(out + row + col) = v;
+    if (out16) {
+      uint16_t hb[4], lb[4];
+      pf16_split_bits(v.x, hb[0], lb[0]);
+      pf16_split_bits(v.y, hb[1], lb[1]);
+      pf16_split_bits(v.z, hb[2], lb[2]);
+      pf16_split_bits(v.w, hb[3], lb[3]);
+      uint16_t* d = out16 + pf16_x_at(row, col);  // col % 4 == 0: four elements of one group
+      *reinterpret_cast<uint2*>(d) = uint2{hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16)};
+      *reinterpret_cast<uint2*>(d + 8) = uint2{lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16)};
+    }
+  }
+}
 
 // NT threads (max(4, group) waves, rounded to 4 or 8); the block's K/V tile
 // for positions j0 .. j0 + 63 is fetched as float4 (16 per position and
@@ -688,12 +746,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
   }
   // O^T tile i, register r: dim 16 i + 4 g + r of query li
   if (live && tq < A.T) {
-    const float inv = 1.0f / l;
-    float* dst = A.out + (size_t)tq * A.n + (size_t)h * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 16; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[16 * i + 4 * g + r] = o[i][r] * inv;
+    pf_attn_store<HD>(o, 1.0f / l, A.out, A.out16, (size_t)tq * A.n, (uint32_t)h * HD, g);
   }
 }
 
@@ -799,6 +852,7 @@ struct PfAttn16 {
   const uint16_t* vh;
   const uint16_t* vl;
   float* out;          // [T][n]
+  uint16_t* out16;     // with it, out in the split-f16 GEMM's interleaved halves too (or null)
   uint32_t T, p0, n, group, cap;
   float scale;         // 1 / sqrt(hd)
 };
@@ -956,12 +1010,7 @@ __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
     }
   }
   if (live && tq < A.T) {
-    const float inv = 1.0f / l;
-    float* dst = A.out + (size_t)tq * A.n + (size_t)h * HD;
-#pragma unroll
-    for (int i = 0; i < HD / 16; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[16 * i + 4 * g + r] = o[i][r] * inv;
+    pf_attn_store<HD>(o, 1.0f / l, A.out, A.out16, (size_t)tq * A.n, (uint32_t)h * HD, g);
   }
 }
 

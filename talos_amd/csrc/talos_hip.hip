@@ -129,6 +129,8 @@ struct talos_hip_ctx {
   // per KV head K [kv_cap][hd] and V^T in 64-position tiles, hi and lo;
   // kv_cap = the context length rounded up to 64
   uint16_t *pf_kh = nullptr, *pf_kl = nullptr, *pf_vh = nullptr, *pf_vl = nullptr;
+  // the split-f16 GEMMs' inputs pf_xn, pf_att, pf_h as interleaved halves
+  uint16_t *pf_xn16 = nullptr, *pf_att16 = nullptr, *pf_h16 = nullptr;
   uint32_t pf_kv_cap = 0;
   int32_t* pf_tok = nullptr;
   bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
@@ -1049,6 +1051,10 @@ int pf_reserve(talos_hip_ctx* c, uint32_t T) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
+  for (uint16_t** p : {&c->pf_xn16, &c->pf_att16, &c->pf_h16}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
   if (c->pf_tok) (void)hipFree(c->pf_tok);
   c->pf_tok = nullptr;
   c->pf_cap = 0;
@@ -1056,6 +1062,10 @@ int pf_reserve(talos_hip_ctx* c, uint32_t T) {
   for (float** p : {&c->pf_x, &c->pf_xn, &c->pf_qr, &c->pf_q, &c->pf_att}) HIPCHK(c, hipMalloc(p, (size_t)T * n * 4));
   for (float** p : {&c->pf_kr, &c->pf_vr}) HIPCHK(c, hipMalloc(p, (size_t)T * kv * 4));
   for (float** p : {&c->pf_g, &c->pf_u, &c->pf_h}) HIPCHK(c, hipMalloc(p, (size_t)T * ff * 4));
+  if (c->pf_f16) {
+    for (uint16_t** p : {&c->pf_xn16, &c->pf_att16}) HIPCHK(c, hipMalloc(p, (size_t)T * n * 4));
+    if (ff % 8 == 0) HIPCHK(c, hipMalloc(&c->pf_h16, (size_t)T * ff * 4));
+  }
   HIPCHK(c, hipMalloc(&c->pf_tok, (size_t)T * 4));
   c->pf_cap = T;
   return TALOS_OK;
@@ -1068,12 +1078,17 @@ struct GemmOut {
   float* y;
   uint32_t ldy;
 };
-void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float* X, uint32_t T, int acc) {
+struct GemmIn {
+  const float* x;       // [T][K]
+  const uint16_t* x16;  // x as the split-f16 GEMM's interleaved halves (or null: only the f32 GEMM)
+};
+void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, GemmIn X, uint32_t T, int acc) {
   const GemmOut* o = outs.begin();
   const size_t n = outs.size();
   for (size_t i = 0; i < n;) {
     PfGemm G{};
-    G.X = X;
+    G.X = X.x;
+    G.X16 = X.x16;
     G.T = T;
     G.K = (uint32_t)o[i].w->cols;
     G.accumulate = acc;
@@ -1095,11 +1110,11 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, const float
     const dim3 grid((T + PF_TOK - 1) / PF_TOK, tiles);
     switch (type) {
       case TALOS_GGML_Q4_0:
-        if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        if (G.X16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
         else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
         break;
       case TALOS_GGML_Q8_0:
-        if (c->pf_f16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        if (G.X16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
         else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
         break;
       case TALOS_GGML_Q6_K: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q6_K>, grid, dim3(PF_NT), 0, c->stream, G); break;
@@ -1114,6 +1129,7 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
   A.kc = c->kc[l];
   A.vc = c->vc[l];
   A.out = c->pf_att;
+  A.out16 = c->pf_att16;
   A.T = T;
   A.p0 = p0;
   A.n = c->cfg.n_embd;
@@ -1145,6 +1161,7 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
     B.vh = c->pf_vh;
     B.vl = c->pf_vl;
     B.out = c->pf_att;
+    B.out16 = c->pf_att16;
     B.T = T;
     B.p0 = p0;
     B.n = c->cfg.n_embd;
@@ -1210,18 +1227,21 @@ int pf_chunk(talos_hip_ctx* c, const uint32_t* tokens, uint32_t T, uint32_t p0) 
   for (uint32_t l = 0; l < cf.n_layer; ++l) {
     LayerW w;
     if ((rc = layer_weights(c, l, &w))) return rc;
-    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.an, cf.rms_eps, n, c->pf_xn);
-    enq_gemm(c, {{w.q, c->pf_qr, n}, {w.k, c->pf_kr, kv}, {w.v, c->pf_vr, kv}}, c->pf_xn, T, 0);
+    const GemmIn xn{c->pf_xn, c->pf_xn16};
+    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.an, cf.rms_eps, n, c->pf_xn,
+                       c->pf_xn16);
+    enq_gemm(c, {{w.q, c->pf_qr, n}, {w.k, c->pf_kr, kv}, {w.v, c->pf_vr, kv}}, xn, T, 0);
     hipLaunchKernelGGL(k_pf_rope_kv, dim3((std::max(n, kv) + 255) / 256, T), dim3(256), 0, c->stream, c->pf_qr,
                        c->pf_kr, c->pf_vr, c->pf_q, c->kc[l], c->vc[l], c->rope, p0, n, cf.n_head, c->hd, kv);
     enq_pf_attn(c, l, T, p0);
-    enq_gemm(c, {{w.o, c->pf_x, n}}, c->pf_att, T, 1);
-    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.fn, cf.rms_eps, n, c->pf_xn);
-    enq_gemm(c, {{w.g, c->pf_g, ff}, {w.u, c->pf_u, ff}}, c->pf_xn, T, 0);
+    enq_gemm(c, {{w.o, c->pf_x, n}}, {c->pf_att, c->pf_att16}, T, 1);
+    hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.fn, cf.rms_eps, n, c->pf_xn,
+                       c->pf_xn16);
+    enq_gemm(c, {{w.g, c->pf_g, ff}, {w.u, c->pf_u, ff}}, xn, T, 0);
     const size_t cnt = (size_t)T * ff;
     hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, c->stream, c->pf_g, c->pf_u,
-                       c->pf_h, cnt);
-    enq_gemm(c, {{w.d, c->pf_x, n}}, c->pf_h, T, 1);
+                       c->pf_h, c->pf_h16, cnt);
+    enq_gemm(c, {{w.d, c->pf_x, n}}, {c->pf_h, c->pf_h16}, T, 1);
   }
   HIPCHK(c, hipGetLastError());
   return TALOS_OK;
@@ -1362,7 +1382,7 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
                  c->samp_ka, c->samp_kb, c->samp_pb, c->samp_out, c->samp_u, c->nll, c->pf_x, c->pf_xn,
                  c->pf_qr, c->pf_q, c->pf_att, c->pf_kr, c->pf_vr, c->pf_g, c->pf_u, c->pf_h, c->pf_tok,
-                 c->pf_kh, c->pf_kl, c->pf_vh, c->pf_vl,
+                 c->pf_kh, c->pf_kl, c->pf_vh, c->pf_vl, c->pf_xn16, c->pf_att16, c->pf_h16,
                  c->mv_x, c->mv_out, c->d_layers, c->d_sync, c->mact, c->mpart, c->qraw, c->kraw,
                  c->vraw, c->graw, c->uraw, c->scores};
   for (void* p : dev)
