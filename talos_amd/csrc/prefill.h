@@ -8,10 +8,13 @@
 //   rmsnorm -> q, k, v = GEMMs -> RoPE, K/V rows into the cache ->
 //   causal attention -> x += GEMM(o) -> rmsnorm -> gate, up = GEMMs ->
 //   SwiGLU -> x += GEMM(down).
-// The GEMMs run on v_mfma_f32_16x16x4_f32 (f32 products and sums, the
-// dequantized weight in f32: exactly the weight the reference multiplies),
-// the attention as a flash-style loop on the same instruction.  Only the
-// chunk's last row goes on to the final norm and the output projection.
+// Q4_0 / Q8_0 GEMMs and the attention run on f16 matrix cores with operands
+// split into hi + lo halves (k_pf_gemm16, k_pf_attn16: f32-level products,
+// f32 sums); F32 and Q6_K matrices, head_dim not a multiple of 32 and
+// TALOS_HIP_PF16=0 take the f32 matrix-core kernels (k_pf_gemm, k_pf_attn:
+// f32 products and sums, the dequantized weight in f32, exactly the weight
+// the reference multiplies).  Only the chunk's last row goes on to the
+// final norm and the output projection.
 //
 // v_mfma_f32_16x16x4_f32 (one wave): D[16][16] += A[16][4] B[4][16] with
 // lane l supplying A[l % 16][l / 16] and B[l / 16][l % 16], and holding
