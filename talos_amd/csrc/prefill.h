@@ -332,17 +332,13 @@ __device__ __forceinline__ pf4 mfma16x32h(pfh8 a, pfh8 b, pf4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// hi + lo halves of v = a * b rounded to f32.  The empty asm statement pins
-// the rounded product in a register: otherwise the compiler may fold the
-// product into v_fma_mixlo_f16 (the exact product rounded once to f16) for
-// the hi that lo is computed from while converting the rounded f32 product
-// for the hi it stores, and where the two roundings differ (an f32 product
-// on an f16 rounding midpoint) hi + lo is off by an f16 ulp.
+// hi + lo halves of v = a * b rounded to f32 (pf16_split_bits: the product
+// pinned before it is split).
 __device__ __forceinline__ void pf16_split_product(float a, float b, _Float16& hi, _Float16& lo) {
-  float v = a * b;
-  asm volatile("" : "+v"(v));
-  hi = (_Float16)v;
-  lo = (_Float16)(v - (float)hi);
+  uint16_t hb, lb;
+  pf16_split_bits(a * b, hb, lb);
+  hi = __builtin_bit_cast(_Float16, hb);
+  lo = __builtin_bit_cast(_Float16, lb);
 }
 
 // This lane's 8 weights of each of the chunk's two blocks as raw bytes (8
