@@ -107,6 +107,12 @@ struct PfGemm {
   const uint16_t* X16;  // X in interleaved halves (pf16_x_at; k_pf_gemm16)
   uint32_t T, K;
   int accumulate;
+  // k_pf_gemm16<FMT, true>: S[0] gate and S[1] up (same rows); a block
+  // owns 64 rows of each and writes H = silu(gate) * up ([T][ldh], and its
+  // interleaved halves H16) instead of Y
+  float* H;
+  uint16_t* H16;
+  uint32_t ldh;
 };
 
 // One lane's weights of a 64-wide K chunk: two 32-element blocks of its row.
@@ -473,18 +479,23 @@ __device__ __forceinline__ void pf16_store_x(const PfX16& P, _Float16* Xh, _Floa
   *reinterpret_cast<u4*>(Xl + tt * PF_HP + 8 * k8) = P.l;
 }
 
-template <uint32_t FMT>
+template <uint32_t FMT, bool SWIGLU = false>
 __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "integer weights only");
-  __shared__ _Float16 Xs[2][2][64 * PF_HP];  // [buffer][hi, lo][token][k]
+  __shared__ __align__(16) _Float16 Xs[2][2][64 * PF_HP];  // [buffer][hi, lo][token][k]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
   uint32_t tile = blockIdx.y, s = 0;
-  while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
+  if (SWIGLU) {
+    s = (uint32_t)wave >> 2;  // waves 0-3: gate rows, 4-7: the same up rows
+  } else {
+    while (s + 1 < G.nseg && tile >= G.S[s].tiles) tile -= G.S[s++].tiles;
+  }
   const PfSeg& S = G.S[s];
   const uint32_t M = S.W.rows;
   const uint32_t tb = blockIdx.x * 64;
-  const uint32_t row = tile * PF_ROWS + (uint32_t)wave * 16 + li;
+  const uint32_t row = SWIGLU ? tile * (PF_ROWS / 2) + (uint32_t)(wave & 3) * 16 + li
+                              : tile * PF_ROWS + (uint32_t)wave * 16 + li;
   const uint32_t rowc = row < M ? row : M - 1;
   pf4 acc[4];
 #pragma unroll
@@ -530,6 +541,34 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
     }
     wc = wn;
     xc = xn;
+  }
+  if constexpr (SWIGLU) {
+    // gate and up tiles meet in LDS ([gate, up][64 rows][64 tokens], pitch
+    // 65), then each thread forms 8 of the block's h = silu(g) * u (the same
+    // f32 operations as k_pf_swiglu), rows fastest for the stores
+    __syncthreads();  // every wave is done with the X tiles
+    float* E = reinterpret_cast<float*>(&Xs[0][0][0]);
+    {
+      const int rl = (wave & 3) * 16 + li;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) E[(s * 64 + rl) * 65 + 16 * t + 4 * g + r] = acc[t][r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int idx = tid + PF_NT * k, rl = idx & 63, tk = idx >> 6;
+      const uint32_t hrow = tile * (PF_ROWS / 2) + (uint32_t)rl, tok = tb + (uint32_t)tk;
+      if (hrow < M && tok < G.T) {
+        const float gv = E[rl * 65 + tk], uv = E[(64 + rl) * 65 + tk];
+        const float hv = (gv / (1.0f + expf(-gv))) * uv;
+        G.H[(size_t)tok * G.ldh + hrow] = hv;
+        const size_t at = pf16_x_at((size_t)tok * G.ldh, hrow);
+        pf16_split_bits(hv, G.H16[at], G.H16[at + 8]);
+      }
+    }
+    return;
   }
   if (row < M) {
 #pragma unroll

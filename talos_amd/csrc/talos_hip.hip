@@ -1123,6 +1123,32 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, GemmIn X, u
   }
 }
 
+// H = silu(X W_gate^T) * (X W_up^T) in one launch when both matrices are
+// Q4_0 or both Q8_0 and X comes split: the split-f16 GEMM with the SwiGLU in
+// its epilogue (k_pf_gemm16<FMT, true>).  Returns false when it does not apply.
+bool enq_gateup_swiglu(talos_hip_ctx* c, const DevWeight* wg, const DevWeight* wu, GemmIn X, uint32_t T) {
+  if (!X.x16 || !c->pf_h16 || wg->type != wu->type || wg->rows != wu->rows || wg->cols != wu->cols ||
+      (wg->type != TALOS_GGML_Q4_0 && wg->type != TALOS_GGML_Q8_0))
+    return false;
+  PfGemm G{};
+  G.X = X.x;
+  G.X16 = X.x16;
+  G.T = T;
+  G.K = (uint32_t)wg->cols;
+  G.nseg = 2;
+  G.S[0].W = wg->mat;
+  G.S[1].W = wu->mat;
+  G.H = c->pf_h;
+  G.H16 = c->pf_h16;
+  G.ldh = (uint32_t)wg->rows;
+  const dim3 grid((T + PF_TOK - 1) / PF_TOK, (uint32_t)((wg->rows + PF_ROWS / 2 - 1) / (PF_ROWS / 2)));
+  if (wg->type == TALOS_GGML_Q4_0)
+    hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q4_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
+  else
+    hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q8_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
+  return true;
+}
+
 void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
   PfAttn A{};
   A.Q = c->pf_q;
@@ -1237,10 +1263,12 @@ int pf_chunk(talos_hip_ctx* c, const uint32_t* tokens, uint32_t T, uint32_t p0) 
     enq_gemm(c, {{w.o, c->pf_x, n}}, {c->pf_att, c->pf_att16}, T, 1);
     hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.fn, cf.rms_eps, n, c->pf_xn,
                        c->pf_xn16);
-    enq_gemm(c, {{w.g, c->pf_g, ff}, {w.u, c->pf_u, ff}}, xn, T, 0);
-    const size_t cnt = (size_t)T * ff;
-    hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, c->stream, c->pf_g, c->pf_u,
-                       c->pf_h, c->pf_h16, cnt);
+    if (!enq_gateup_swiglu(c, w.g, w.u, xn, T)) {
+      enq_gemm(c, {{w.g, c->pf_g, ff}, {w.u, c->pf_u, ff}}, xn, T, 0);
+      const size_t cnt = (size_t)T * ff;
+      hipLaunchKernelGGL(k_pf_swiglu, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, c->stream, c->pf_g,
+                         c->pf_u, c->pf_h, c->pf_h16, cnt);
+    }
     enq_gemm(c, {{w.d, c->pf_x, n}}, {c->pf_h, c->pf_h16}, T, 1);
   }
   HIPCHK(c, hipGetLastError());
