@@ -163,3 +163,29 @@ def test_prefill_q6k_and_mixed_formats(talos, oracle, case):
     record_parity(f"{case}_batched_prefill_{n}", max(d, dk), 1e-3, path="batched_prefill")
     ref.close()
     m.close()
+
+
+@pytest.mark.parametrize("which,n", [("gqa_q8", 300), ("mistral7b_q4", 40)])
+def test_prefill_f32_matrix_cores(talos, oracle, monkeypatch, which, n):
+    """TALOS_HIP_PF16=0: the Q4_0 / Q8_0 GEMMs and the attention on the f32
+    matrix cores (k_pf_gemm, a separate SwiGLU pass, k_pf_attn) -- the
+    fallback of the split-f16 kernels -- against the oracle's token loop."""
+    from talos_amd import configs
+    monkeypatch.setenv("TALOS_HIP_PF16", "0")
+    wl = getattr(configs, which)() if which != "mistral7b_q4" else configs.mistral7b_q4(ctx=128)
+    _step(f"{which}: {n}-token prompt on f32 matrix cores")
+    m = talos.Model.synth(wl.spec, nthreads=16)
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=16)
+    prompt = [int(t) for t in np.random.default_rng(wl.spec.seed + 5).integers(0, wl.spec.vocab_size, n)]
+    lg, am = m.prefill(prompt, 0)
+    for p, t in enumerate(prompt):
+        c = ref.forward(t, p)
+    kg, vg = m.kv_read(n)
+    kc, vc = ref.get_kv(n)
+    d = float(np.abs(lg - c).max())
+    dk = float(max(np.abs(kg - kc).max(), np.abs(vg - vc).max()))
+    print(f"  last logits max abs {d:.3e}, K/V max abs {dk:.3e}; argmax gpu {am} cpu {oracle.argmax(c)}", flush=True)
+    assert d <= 1e-3 and dk <= 1e-3 and am == oracle.argmax(c)
+    record_parity(f"{which}_f32mfma_prefill_{n}", max(d, dk), 1e-3, path="batched_prefill")
+    ref.close()
+    m.close()
