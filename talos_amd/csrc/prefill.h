@@ -901,9 +901,10 @@ struct PfAttn16 {
 // LDS between two block syncs.  At most 256 registers per lane, so that two
 // waves share each SIMD (two 4-wave blocks per CU: 13.8k against 12.4k
 // tok/s at the 7B shape's 16k prompt, where the unbounded build took 259).
-template <int HD, int NT>
+template <int HD, int NT, int QG = 1>
 __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
   static_assert(HD % 32 == 0 && (16 * HD) % NT == 0, "head_dim a multiple of 32");
+  constexpr int WPQ = NT / 64 / QG;   // waves per group of 16 queries
   constexpr int KP = HD + 8;          // K halves pitch (conflict-free row reads)
   constexpr int VP = PF_ATT_KT + 8;   // V^T halves pitch
   constexpr int PC = 16 * HD / NT;    // 16-byte pieces per thread, each of K and V
@@ -914,10 +915,13 @@ __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
   _Float16* Vl = Vh + HD * VP;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, li = lane & 15;
-  const uint32_t kvh = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * PF_ATT_Q;
-  const uint32_t h = kvh * A.group + (uint32_t)wave;
-  const bool live = (uint32_t)wave < A.group;
-  const uint32_t tq = t0 + li;
+  // QG groups of 16 queries per block, each with one wave per q head (the
+  // K/V tile in LDS serves QG times the matrix work)
+  const int qg = wave / WPQ, hw = wave % WPQ;
+  const uint32_t kvh = blockIdx.x, t0 = (gridDim.y - 1 - blockIdx.y) * (PF_ATT_Q * QG);
+  const uint32_t h = kvh * A.group + (uint32_t)hw;
+  const bool live = (uint32_t)hw < A.group;
+  const uint32_t tq = t0 + PF_ATT_Q * qg + li;
   const int qpos = (int)(A.p0 + (tq < A.T ? tq : A.T - 1));
   constexpr float kLog2e = 1.4426950408889634f;
   // Q^T fragments of step s: Q[query li][32 s + 8 g .. +7], pre-scaled, split
@@ -944,7 +948,7 @@ __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
   for (int i = 0; i < HD / 16; ++i) o[i] = pf4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   const int first = (int)(A.p0 + t0);  // the block's earliest query position
-  const int last = (int)(A.p0 + min(t0 + PF_ATT_Q, A.T) - 1);
+  const int last = (int)(A.p0 + min(t0 + PF_ATT_Q * QG, A.T) - 1);
   u4 kr[PC], vr[PC];
   // K piece e: array e / (8 HD) (hi, lo), position (e / (HD / 8)) % 64,
   // channels 8 (e % (HD / 8)) .. +7; V piece e: array e / (8 HD), channel

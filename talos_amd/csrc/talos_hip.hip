@@ -1195,11 +1195,16 @@ void enq_pf_attn(talos_hip_ctx* c, uint32_t l, uint32_t T, uint32_t p0) {
     B.cap = c->pf_kv_cap;
     B.scale = A.scale;
     const size_t lds16 = pf_attn16_lds_bytes(c->hd);
+    // 8 waves: groups of up to 4 q heads take two 16-query groups per block
+    // (the K/V tile staged once for twice the matrix work), larger groups one
+    const bool two = c->group <= 4;
+    const uint32_t qb = PF_ATT_Q * (two ? 2 : 1);
+    const dim3 grid16(c->cfg.n_head_kv, (T + qb - 1) / qb), block16(512);
     switch (c->hd / 32) {
-#define PF_ATT16_CASE(N)                                                                          \
-  case N:                                                                                         \
-    if (wide) hipLaunchKernelGGL((k_pf_attn16<32 * N, 512>), grid, block, lds16, c->stream, B);  \
-    else hipLaunchKernelGGL((k_pf_attn16<32 * N, 256>), grid, block, lds16, c->stream, B);       \
+#define PF_ATT16_CASE(N)                                                                                  \
+  case N:                                                                                                 \
+    if (two) hipLaunchKernelGGL((k_pf_attn16<32 * N, 512, 2>), grid16, block16, lds16, c->stream, B);    \
+    else hipLaunchKernelGGL((k_pf_attn16<32 * N, 512, 1>), grid16, block16, lds16, c->stream, B);        \
     break;
       PF_ATT16_CASE(1) PF_ATT16_CASE(2) PF_ATT16_CASE(3) PF_ATT16_CASE(4) PF_ATT16_CASE(5) PF_ATT16_CASE(6)
       PF_ATT16_CASE(7) PF_ATT16_CASE(8)
@@ -1227,9 +1232,9 @@ void set_pf_attn_lds(int bytes) {
 #define PF_ATT_SET(N)                                        \
   set_max_lds((const void*)k_pf_attn<16 * N, 256>, bytes); \
   set_max_lds((const void*)k_pf_attn<16 * N, 512>, bytes);
-#define PF_ATT16_SET(N)                                        \
-  set_max_lds((const void*)k_pf_attn16<32 * N, 256>, bytes); \
-  set_max_lds((const void*)k_pf_attn16<32 * N, 512>, bytes);
+#define PF_ATT16_SET(N)                                           \
+  set_max_lds((const void*)k_pf_attn16<32 * N, 512, 2>, bytes); \
+  set_max_lds((const void*)k_pf_attn16<32 * N, 512, 1>, bytes);
   PF_ATT16_SET(1) PF_ATT16_SET(2) PF_ATT16_SET(3) PF_ATT16_SET(4) PF_ATT16_SET(5) PF_ATT16_SET(6)
   PF_ATT16_SET(7) PF_ATT16_SET(8)
 #undef PF_ATT16_SET
