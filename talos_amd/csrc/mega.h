@@ -284,10 +284,12 @@ struct MegaX {
   XStage X;
   int need;
   __device__ __forceinline__ MegaX(float* smem, int n, int need_) : X(carve_x(smem, n, need_)), need(need_) {}
-  template <class Src, class After, class Wait>
-  __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
-                                        int hi, After after, Wait wait) const {
+  // (the f32 staging applies the rmsnorm factor itself: returns 1)
+  template <bool DEFER = false, class Src, class After, class Wait>
+  __device__ __forceinline__ float stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
+                                         int hi, After after, Wait wait) const {
     mega_stage(src, n, w, eps, norm, X, need, pub, lo, hi, after, wait);
+    return 1.f;
   }
   __device__ __forceinline__ XF src(int layout) const { return XF{X.xs[layout], X.xsum}; }
 };
@@ -295,16 +297,18 @@ template <>
 struct MegaX<true> {
   XQ X;
   __device__ __forceinline__ MegaX(float* smem, int n, int) : X(carve_xq(smem, n, MEGA_GPB, MEGA_NW)) {}
-  template <class Src, class After, class Wait>
-  __device__ __forceinline__ void stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
-                                        int hi, After after, Wait wait) const {
+  // DEFER: returns the rmsnorm factor for the caller to apply to each row
+  // result (stage_xq); otherwise 1.
+  template <bool DEFER = false, class Src, class After, class Wait>
+  __device__ __forceinline__ float stage(Src src, int n, const float* w, float eps, bool norm, float* pub, int lo,
+                                         int hi, After after, Wait wait) const {
     const int n8 = n >> 3;
     if (n8 <= MEGA_NT)
-      stage_xq<1, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
+      return stage_xq<1, MEGA_NT, true, DEFER>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
     else if (n8 <= 2 * MEGA_NT)
-      stage_xq<2, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
+      return stage_xq<2, MEGA_NT, true, DEFER>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
     else
-      stage_xq<4, MEGA_NT, true>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
+      return stage_xq<4, MEGA_NT, true, DEFER>(src, n, w, eps, norm, X, pub, lo, hi, after, wait);
   }
   __device__ __forceinline__ XI src(int) const {
     return XI{reinterpret_cast<const uint8_t*>(X.pl), X.bs, X.nb, 0};
@@ -817,6 +821,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
       auto arr = [&] {
         if (l > 0) arrive();
       };
+      float rs = 1.f;  // rmsnorm factor of the staged x, applied per row
       auto stage = [&](auto&& pf) {
         if (l > 0) {
           // x = (base + attproj) + down of the previous layer; publish it
@@ -829,20 +834,20 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
             if (P.dsplit == 2) {
               Src6 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_dq(P, l - 1, 0),
                        mega_dq(P, l - 1, 1),   mega_dq(P, l - 1, 2),              mega_dq(P, l - 1, 3)};
-              X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
+              rs = X.template stage<true>(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
               done = true;
             }
           }
           if (!done) {
             Src3 src{mega_base(P, l - 1), mega_act(P, l - 1, MEGA_ACT_O), mega_act(P, l - 1, MEGA_ACT_D)};
-            X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
+            rs = X.template stage<true>(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, w);
           }
         } else if (P.embed) {
           EmbSrc src{P.embd, tok};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [] {});
+          rs = X.template stage<true>(src, P.n, LP->attn_norm, P.eps, true, base, pub_lo, pub_hi, pf, [] {});
         } else {
           Src1 src{P.x};
-          X.stage(src, P.n, LP->attn_norm, P.eps, true, nullptr, 0, 0, pf, [] {});
+          rs = X.template stage<true>(src, P.n, LP->attn_norm, P.eps, true, nullptr, 0, 0, pf, [] {});
         }
         MEGA_MARK(P, l * MEGA_TL_PER_LAYER + 0);
       };
@@ -855,7 +860,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
 #pragma unroll
         for (int r = 0; r < RL; r += 2) {
           const uint32_t row = r0 + r;
-          const float y0 = y[r], y1 = y[r + 1];
+          const float y0 = y[r] * rs, y1 = y[r + 1] * rs;
           // (loaded for v rows too: a load under the branch would cost the
           // streaming loop its exact wait counts)
           const uint32_t i = (row % P.hd) / 2;
@@ -1049,9 +1054,10 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
         r0 = pair0(k) * PR;
         rmax = LP->g.rows;
       };
+      float rs = 1.f;  // rmsnorm factor of the staged x, applied per row
       auto stage = [&](auto&& pf) {
         Src2 src{base, o_out};
-        X.stage(src, P.n, LP->ffn_norm, P.eps, true, nullptr, 0, 0, pf, [&] {
+        rs = X.template stage<true>(src, P.n, LP->ffn_norm, P.eps, true, nullptr, 0, 0, pf, [&] {
           wait();
           MEGA_MARK(P, l * MEGA_TL_PER_LAYER + MEGA_TL_BAR + 2);
         });
@@ -1063,7 +1069,7 @@ __global__ __launch_bounds__(MEGA_NT) void k_mega(MegaParams P) {
 #pragma unroll
         for (int r = 0; r < PR; ++r) {
           if (p0 + r < P.ff) {
-            const float g = y[2 * r], u = y[2 * r + 1];
+            const float g = y[2 * r] * rs, u = y[2 * r + 1] * rs;
             st_coh(h + p0 + r, mega_swiglu(g, u));
           }
         }

@@ -67,9 +67,14 @@ __device__ __forceinline__ XQ carve_xq(float* smem, int n, int gpb_max, int nwav
 // Plane layout: [3][nb][32] bytes, or with SPLIT [3][2][nb] 16-byte words
 // (word h of block b at (h * nb + b) * 16: a wave reading one block per lane
 // touches consecutive words, free of LDS bank conflicts).
-template <int NR, int NT, bool SPLIT = false, class Src, class After, class Wait>
-__device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict__ w, float eps, bool norm,
-                                         const XQ& X, float* pub, int pub_lo, int pub_hi, After after, Wait wait) {
+// DEFER (with norm): the planes are those of x*w, and the returned factor
+// 1/sqrt(mean(x^2) + eps) is left for the caller to apply to each matvec
+// result (the planes of a block do not depend on a common factor, so the
+// sum of squares shares the staging's last block sync instead of taking two
+// of its own).  Otherwise the planes are of (x*r)*w and the factor is 1.
+template <int NR, int NT, bool SPLIT = false, bool DEFER = false, class Src, class After, class Wait>
+__device__ __forceinline__ float stage_xq(Src src, int n, const float* __restrict__ w, float eps, bool norm,
+                                          const XQ& X, float* pub, int pub_lo, int pub_hi, After after, Wait wait) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int n8 = n >> 3;
@@ -125,8 +130,13 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
 #pragma unroll
       for (int h = 0; h < 2; ++h)
         ss += v[r][h].x * v[r][h].x + v[r][h].y * v[r][h].y + v[r][h].z * v[r][h].z + v[r][h].w * v[r][h].w;
-    ss = block_sum(ss, X.red, NT / 64);
-    scale = 1.0f / sqrtf(ss / (float)n + eps);
+    if constexpr (DEFER) {
+      ss = wave_sum(ss);
+      if ((tid & 63) == 0) X.red[tid >> 6] = ss;  // read after the closing sync
+    } else {
+      ss = block_sum(ss, X.red, NT / 64);
+      scale = 1.0f / sqrtf(ss / (float)n + eps);
+    }
   }
   if (tid < 4) reinterpret_cast<uint32_t*>(X.zero)[tid] = 0u;
 #pragma unroll
@@ -200,6 +210,10 @@ __device__ __forceinline__ void stage_xq(Src src, int n, const float* __restrict
     }
   }
   __syncthreads();
+  if (!DEFER || !norm) return 1.f;
+  float t = 0.f;  // block_sum's order
+  for (int k = 0; k < NT / 64; ++k) t += X.red[k];
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(1.0f / sqrtf(t / (float)n + eps))));
 }
 
 // One item: U tiles of 4 consecutive Q4_0 blocks of one 16-row group.  Lane
