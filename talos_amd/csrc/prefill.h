@@ -751,8 +751,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
         if (j > qpos) st[u][r] = -INFINITY;
         mx = fmaxf(mx, st[u][r]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float mn = fmaxf(m, mx);
     const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
     m = mn;
@@ -765,8 +764,7 @@ __global__ __launch_bounds__(NT) void k_pf_attn(PfAttn A) {
         st[u][r] = p;
         ps += p;
       }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = xor32_sum(xor16_sum(ps));
     l = l * alpha + ps;
 #pragma unroll
     for (int i = 0; i < HD / 16; ++i) o[i] *= alpha;
@@ -1011,8 +1009,7 @@ __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[u][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float mn = fmaxf(m, mx);
     const float alpha = __builtin_amdgcn_exp2f(m - mn);
     m = mn;
@@ -1025,8 +1022,7 @@ __global__ __launch_bounds__(NT, 2) void k_pf_attn16(PfAttn16 A) {
         st[u][r] = pv;
         ps += pv;
       }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = xor32_sum(xor16_sum(ps));
     l = l * alpha + ps;
 #pragma unroll
     for (int i = 0; i < HD / 16; ++i) o[i] *= alpha;
