@@ -68,9 +68,6 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
-// Sum over the 64 lanes of a wave (row sums, then rows 0+1 into row 1,
-// 2+3 into row 3, then row 1 into rows 2-3; lane 63 holds the total);
-// every lane receives the total.
 // x combined with the x of lane ^ 16 (lane ^ 32) by a commutative op, the
 // same bits in both lanes of a pair: v_permlane16_swap (v_permlane32_swap)
 // with x as both operands leaves each lane's own and partner values in the
@@ -92,6 +89,9 @@ __device__ __forceinline__ float xor32_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Sum over the 64 lanes of a wave (row sums, then rows 0+1 into row 1,
+// 2+3 into row 3, then row 1 into rows 2-3; lane 63 holds the total);
+// every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
   v = row_sum16(v);
   v += dpp_f<DPP_ROW_BCAST15, 0xA>(0.f, v);
