@@ -98,6 +98,10 @@ struct PfSeg {
   float* Y;       // [T][ldy]
   uint32_t ldy;
   uint32_t tiles;  // ceil(W.rows / PF_ROWS)
+  // W's tiled copy (k_pf_tile; Q4_0 / Q8_0 with rows % 16 == 0 and
+  // cols % 64 == 0), or null: the split-f16 GEMM then reads W itself
+  const uint8_t* tq;
+  const uint32_t* td;
 };
 
 struct PfGemm {
@@ -401,6 +405,69 @@ __device__ __forceinline__ void pf16_load_w(PfW16& F, const DevMat& W, uint32_t 
   // 14 % off the 1024-token gate/up GEMM)
   F.d = nb % 2 ? dd[0] | (dd[1] << 16) : *reinterpret_cast<const uint32_t*>(W.d + (size_t)rowc * nb + k0 / 32);
 }
+// The tiled copy of a Q4_0 / Q8_0 matrix (rows % 16 == 0, cols % 64 == 0):
+// piece t = ((r / 16) * (cols / 64) + c) * 16 + r % 16 holds row r's
+// 64-element chunk c, its two blocks' quant bytes (QB = 64 for Q8_0, 32 for
+// Q4_0) at tq + QB t and their two f16 scales as one word td[t].  A wave's
+// 16 rows of a chunk are then one contiguous run (1 KB for Q8_0): each load
+// instruction of pf16_load_w touches 8 (Q8_0) or 4 (Q4_0) whole lines
+// instead of a part of 16 rows' lines each, and the address unit, which the
+// split-f16 GEMM's loads run short of, makes half the passes or fewer.
+template <uint32_t FMT>
+constexpr uint32_t pf_tile_qb() {
+  return FMT == TALOS_FMT_Q8_0 ? 64u : 32u;
+}
+static inline __host__ __device__ size_t pf_tile_bytes(uint32_t fmt, size_t rows, size_t cols) {
+  return rows * (cols / 64) * ((fmt == TALOS_FMT_Q8_0 ? 64 : 32) + 4);
+}
+// One thread per piece, consecutive threads writing consecutive pieces.
+template <uint32_t FMT>
+__global__ __launch_bounds__(256) void k_pf_tile(DevMat W, uint8_t* __restrict__ tq, uint32_t* __restrict__ td) {
+  constexpr uint32_t QB = pf_tile_qb<FMT>();
+  const uint32_t nch = W.cols / 64, nb = W.cols / 32;
+  const size_t total = (size_t)W.rows * nch;
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const uint32_t li = (uint32_t)(t % 16);
+  const size_t rc = t / 16;  // (r / 16) * nch + c
+  const uint32_t r = (uint32_t)(rc / nch) * 16 + li, c = (uint32_t)(rc % nch);
+  const size_t ci = (size_t)r * nb + 2 * c;  // the chunk's first block
+  const u4* src = reinterpret_cast<const u4*>(W.q + ci * (QB / 2));
+  u4* dst = reinterpret_cast<u4*>(tq + t * QB);
+#pragma unroll
+  for (uint32_t i = 0; i < QB / 16; ++i) dst[i] = src[i];
+  td[t] = *reinterpret_cast<const uint32_t*>(W.d + ci);
+}
+// pf16_load_w from the tiled copy (same lane contents).
+template <uint32_t FMT>
+__device__ __forceinline__ void pf16_load_w_tiled(PfW16& F, const PfSeg& S, uint32_t rowc, uint32_t k0, uint32_t K,
+                                                  int g) {
+  const size_t t = ((size_t)(rowc >> 4) * (K / 64) + k0 / 64) * 16 + (rowc & 15);
+  if (FMT == TALOS_FMT_Q8_0) {
+    const u4 v = *reinterpret_cast<const u4*>(S.tq + t * 64 + 16 * g);
+    F.q[0][0] = v.x;
+    F.q[0][1] = v.y;
+    F.q[1][0] = v.z;
+    F.q[1][1] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(S.tq + t * 32 + 8 * g);
+    F.q[0][0] = v.x;
+    F.q[0][1] = v.y;
+  }
+  F.d = S.td[t];
+}
+// (TILED a template parameter, not a test of S.tq: a load under a branch
+// would leave the compiler waiting for every load in flight where the
+// branches meet, the next chunk's weights included)
+template <uint32_t FMT, bool TILED>
+__device__ __forceinline__ void pf16_load_seg(PfW16& F, const PfSeg& S, uint32_t rowc, uint32_t k0, uint32_t K,
+                                              int g) {
+  if constexpr (TILED)
+    pf16_load_w_tiled<FMT>(F, S, rowc, k0, K, g);
+  else
+    pf16_load_w<FMT>(F, S.W, rowc, k0, K, g);
+}
+
 // After the one-load fetch of a Q8_0 chunk, lane group g holds bytes
 // 16 g .. +15 of the chunk (groups 0, 1: block 0; groups 2, 3: block 1).
 // v_permlane32_swap trades the upper 32 lanes of its first operand for the
@@ -479,7 +546,7 @@ __device__ __forceinline__ void pf16_store_x(const PfX16& P, _Float16* Xh, _Floa
   *reinterpret_cast<u4*>(Xl + tt * PF_HP + 8 * k8) = P.l;
 }
 
-template <uint32_t FMT, bool SWIGLU = false>
+template <uint32_t FMT, bool SWIGLU = false, bool TILED = false>
 __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   static_assert(FMT == TALOS_FMT_Q4_0 || FMT == TALOS_FMT_Q8_0, "integer weights only");
   __shared__ __align__(16) _Float16 Xs[2][2][64 * PF_HP];  // [buffer][hi, lo][token][k]
@@ -509,7 +576,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   const int kg = q8one ? ((g & 1) << 1) | (g >> 1) : g;
   PfW16 wc, wn;
   PfX16 xc, xn;
-  pf16_load_w<FMT>(wc, S.W, rowc, 0, G.K, g);
+  pf16_load_seg<FMT, TILED>(wc, S, rowc, 0, G.K, g);
   pf16_load_x(xc, G.X16, G.T, G.K, tb, 0, tid);
   for (int c = 0; c < nchunks; ++c) {
     _Float16* Xh = Xs[c & 1][0];
@@ -520,7 +587,7 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
     pf16_load_x(xn, G.X16, G.T, G.K, tb, kn, tid);
     pf16_store_x(xc, Xh, Xl, tid);
     __syncthreads();
-    pf16_load_w<FMT>(wn, S.W, rowc, kn, G.K, g);
+    pf16_load_seg<FMT, TILED>(wn, S, rowc, kn, G.K, g);
     if (q8one) pf16_swap_q8(wc);
     if (FMT == TALOS_FMT_Q4_0 && one) pf16_swap_q4(wc);
 #pragma unroll

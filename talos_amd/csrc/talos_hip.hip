@@ -70,6 +70,7 @@ struct DevWeight {
   void* mem = nullptr;
   DevMat mat{};
   const float* f32 = nullptr;  // F32 tensors: the plain row-major data
+  void* tiled = nullptr;       // the prefill GEMMs' tiled copy, in the context's pool (pf_tile_weights), or null
 };
 
 // G_TOKEN: embedding on the device + argmax; G_GREEDY: + greedy advance;
@@ -136,6 +137,8 @@ struct talos_hip_ctx {
   bool allow_batch = true;  // TALOS_HIP_BATCH=0: prompts one step per token
   bool pf_f16 = true;       // TALOS_HIP_PF16=0: Q4_0/Q8_0 prefill GEMMs on f32 MFMA instead of split f16
   bool pf_attn16 = true;    // TALOS_HIP_PFA16=0: prefill attention on f32 MFMA instead of split f16
+  bool pf_tiled = true;     // TALOS_HIP_PF_TILED=0: the split-f16 GEMMs read the weights without tiled copies
+  void* pf_tile_pool = nullptr;  // every tiled copy (one allocation), or null
   float* mv_x = nullptr;  // standalone matvec staging
   float* mv_out = nullptr;
   size_t mv_x_cap = 0, mv_out_cap = 0;
@@ -1071,6 +1074,69 @@ int pf_reserve(talos_hip_ctx* c, uint32_t T) {
   return TALOS_OK;
 }
 
+// The tiled copies the split-f16 GEMMs read (k_pf_tile): made for every
+// Q4_0 / Q8_0 layer matrix with rows % 16 == 0 and cols % 64 == 0 at the
+// first batched prefill, in one allocation -- one more device copy of those
+// matrices, kept until a weight is uploaded (pf_tile_drop) or the context is
+// destroyed.  When the pool does not fit the device the GEMMs read the
+// matrices themselves.
+static bool pf_tileable(const DevWeight* w) {
+  return (w->type == TALOS_GGML_Q4_0 || w->type == TALOS_GGML_Q8_0) && w->rows % 16 == 0 && w->cols % 64 == 0;
+}
+int pf_tile_weights(talos_hip_ctx* c) {
+  if (!c->pf_f16 || !c->pf_tiled || c->pf_tile_pool) return TALOS_OK;
+  std::vector<DevWeight*> ms;
+  size_t total = 0;
+  for (uint32_t l = 0; l < c->cfg.n_layer; ++l) {
+    LayerW w;
+    int rc = layer_weights(c, l, &w);
+    if (rc) return rc;
+    for (const DevWeight* cw : {w.q, w.k, w.v, w.o, w.g, w.u, w.d}) {
+      if (!pf_tileable(cw)) continue;
+      ms.push_back(const_cast<DevWeight*>(cw));  // the weights live in c->weights, which is not const
+      total += (pf_tile_bytes(cw->type, cw->rows, cw->cols) + 255) / 256 * 256;
+    }
+  }
+  if (ms.empty()) return TALOS_OK;
+  if (hipMalloc(&c->pf_tile_pool, total) != hipSuccess) {
+    (void)hipGetLastError();
+    c->pf_tile_pool = nullptr;
+    return TALOS_OK;
+  }
+  uint8_t* p = static_cast<uint8_t*>(c->pf_tile_pool);
+  for (DevWeight* m : ms) {
+    m->tiled = p;
+    const size_t qb = m->type == TALOS_GGML_Q8_0 ? 64 : 32, pieces = m->rows * (m->cols / 64);
+    uint32_t* td = reinterpret_cast<uint32_t*>(p + pieces * qb);
+    const dim3 grid((unsigned)((pieces + 255) / 256));
+    if (m->type == TALOS_GGML_Q8_0)
+      hipLaunchKernelGGL(k_pf_tile<TALOS_FMT_Q8_0>, grid, dim3(256), 0, c->stream, m->mat, p, td);
+    else
+      hipLaunchKernelGGL(k_pf_tile<TALOS_FMT_Q4_0>, grid, dim3(256), 0, c->stream, m->mat, p, td);
+    HIPCHK(c, hipGetLastError());
+    p += (pf_tile_bytes(m->type, m->rows, m->cols) + 255) / 256 * 256;
+  }
+  return TALOS_OK;
+}
+// Every tiled copy goes (an upload may change any matrix); the next batched
+// prefill makes them again.
+void pf_tile_drop(talos_hip_ctx* c) {
+  if (!c->pf_tile_pool) return;
+  (void)hipStreamSynchronize(c->stream);
+  (void)hipFree(c->pf_tile_pool);
+  c->pf_tile_pool = nullptr;
+  for (auto& kv : c->weights) kv.second.tiled = nullptr;
+}
+void pf_seg_tiled(PfSeg& S, const DevWeight* w) {
+  if (!w->tiled) {
+    S.tq = nullptr;
+    S.td = nullptr;
+    return;
+  }
+  S.tq = static_cast<const uint8_t*>(w->tiled);
+  S.td = reinterpret_cast<const uint32_t*>(S.tq + w->rows * (w->cols / 64) * (w->type == TALOS_GGML_Q8_0 ? 64 : 32));
+}
+
 // Y_i[T][ldy_i] (+)= X[T][K] W_i^T for matrices sharing X; consecutive ones
 // of one format go out as one launch (up to three).
 struct GemmOut {
@@ -1097,6 +1163,7 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, GemmIn X, u
     while (i < n && G.nseg < 3 && o[i].w->type == type) {
       PfSeg& S = G.S[G.nseg++];
       S.W = o[i].w->mat;
+      pf_seg_tiled(S, o[i].w);
       S.Y = o[i].y;
       S.ldy = o[i].ldy;
       S.tiles = (uint32_t)((o[i].w->rows + PF_ROWS - 1) / PF_ROWS);
@@ -1108,14 +1175,24 @@ void enq_gemm(talos_hip_ctx* c, std::initializer_list<GemmOut> outs, GemmIn X, u
     // token tiles of X and a row tile's weights are fetched about once per
     // XCD (+0.6 % at a 16k prompt against row tiles on x)
     const dim3 grid((T + PF_TOK - 1) / PF_TOK, tiles);
+    bool tiled = true;  // every segment has its tiled copy
+    for (uint32_t s = 0; s < G.nseg; ++s) tiled = tiled && G.S[s].tq;
     switch (type) {
       case TALOS_GGML_Q4_0:
-        if (G.X16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
-        else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        if (G.X16 && tiled)
+          hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q4_0, false, true>), grid, dim3(PF_NT), 0, c->stream, G);
+        else if (G.X16)
+          hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        else
+          hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q4_0>, grid, dim3(PF_NT), 0, c->stream, G);
         break;
       case TALOS_GGML_Q8_0:
-        if (G.X16) hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
-        else hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        if (G.X16 && tiled)
+          hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q8_0, false, true>), grid, dim3(PF_NT), 0, c->stream, G);
+        else if (G.X16)
+          hipLaunchKernelGGL(k_pf_gemm16<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
+        else
+          hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q8_0>, grid, dim3(PF_NT), 0, c->stream, G);
         break;
       case TALOS_GGML_Q6_K: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_Q6_K>, grid, dim3(PF_NT), 0, c->stream, G); break;
       default: hipLaunchKernelGGL(k_pf_gemm<TALOS_FMT_F32>, grid, dim3(PF_NT), 0, c->stream, G); break;
@@ -1138,14 +1215,24 @@ bool enq_gateup_swiglu(talos_hip_ctx* c, const DevWeight* wg, const DevWeight* w
   G.nseg = 2;
   G.S[0].W = wg->mat;
   G.S[1].W = wu->mat;
+  pf_seg_tiled(G.S[0], wg);
+  pf_seg_tiled(G.S[1], wu);
   G.H = c->pf_h;
   G.H16 = c->pf_h16;
   G.ldh = (uint32_t)wg->rows;
   const dim3 grid((T + PF_TOK - 1) / PF_TOK, (uint32_t)((wg->rows + PF_ROWS / 2 - 1) / (PF_ROWS / 2)));
-  if (wg->type == TALOS_GGML_Q4_0)
-    hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q4_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
-  else
-    hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q8_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
+  const bool tiled = G.S[0].tq && G.S[1].tq;
+  if (wg->type == TALOS_GGML_Q4_0) {
+    if (tiled)
+      hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q4_0, true, true>), grid, dim3(PF_NT), 0, c->stream, G);
+    else
+      hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q4_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
+  } else {
+    if (tiled)
+      hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q8_0, true, true>), grid, dim3(PF_NT), 0, c->stream, G);
+    else
+      hipLaunchKernelGGL((k_pf_gemm16<TALOS_FMT_Q8_0, true>), grid, dim3(PF_NT), 0, c->stream, G);
+  }
   return true;
 }
 
@@ -1340,6 +1427,8 @@ int talos_hip_create(const talos_hip_cfg* cfg, talos_hip_ctx** out) {
   c->pf_f16 = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_PFA16");
   c->pf_attn16 = !(env && env[0] == '0');
+  env = getenv("TALOS_HIP_PF_TILED");
+  c->pf_tiled = !(env && env[0] == '0');
   env = getenv("TALOS_HIP_ATTN_DIRECT");
   if (env) c->attn_direct = std::max(0, atoi(env));
   c->hd = hd;
@@ -1410,6 +1499,7 @@ void talos_hip_destroy(talos_hip_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   destroy_graphs(c);
   for (auto& kv : c->weights) (void)hipFree(kv.second.mem);
+  if (c->pf_tile_pool) (void)hipFree(c->pf_tile_pool);
   for (float* p : c->kc) (void)hipFree(p);
   for (float* p : c->vc) (void)hipFree(p);
   void* dev[] = {c->io, c->q, c->atty, c->h, c->logits, c->hidden, c->part, c->count, c->tokens, c->rope,
@@ -1475,6 +1565,7 @@ int talos_hip_upload_weight(talos_hip_ctx* c, const char* name, const void* byte
     c->weights.emplace(name, w);
   }
   destroy_graphs(c);  // graphs captured the old pointers
+  pf_tile_drop(c);
   c->mega_ready = false;
   return TALOS_OK;
 }
@@ -1589,6 +1680,7 @@ int talos_hip_prefill(talos_hip_ctx* c, const uint32_t* tokens, uint32_t n, uint
     // token's row then takes the final norm, the output projection and the
     // argmax as a decode step's head does
     if ((rc = pf_reserve(c, std::min(n, (uint32_t)PF_CHUNK)))) return rc;
+    if ((rc = pf_tile_weights(c))) return rc;
     uint32_t last = 0;
     for (uint32_t c0 = 0; c0 < n; c0 += PF_CHUNK) {
       const uint32_t T = std::min((uint32_t)PF_CHUNK, n - c0);

@@ -189,3 +189,40 @@ def test_prefill_f32_matrix_cores(talos, oracle, monkeypatch, which, n):
     record_parity(f"{which}_f32mfma_prefill_{n}", max(d, dk), 1e-3, path="batched_prefill")
     ref.close()
     m.close()
+
+
+@pytest.mark.parametrize("which,n", [("gqa_q8", 300), ("mistral7b_q4", 40)])
+def test_prefill_tiled_weights_bit_identical(talos, oracle, monkeypatch, which, n):
+    """The split-f16 GEMMs reading the tiled weight copies (the default) give
+    the same bits as reading the row-major matrices (TALOS_HIP_PF_TILED=0):
+    each lane loads the same bytes either way.  Both against the oracle's
+    token loop as well.  (gqa_q8's down-projection, 1376 columns, has no
+    tiled copy: that launch reads the matrix itself in both runs.)"""
+    from talos_amd import configs
+    wl = getattr(configs, which)() if which != "mistral7b_q4" else configs.mistral7b_q4(ctx=128)
+    prompt = [int(t) for t in np.random.default_rng(wl.spec.seed + 7).integers(0, wl.spec.vocab_size, n)]
+    monkeypatch.setenv("TALOS_HIP_PF_TILED", "1")
+    _step(f"{which}: {n}-token prompt, tiled weight copies")
+    m = talos.Model.synth(wl.spec, nthreads=16)
+    lt, at = m.prefill(prompt, 0)
+    kt, vt = m.kv_read(n)
+    lt, kt, vt = lt.copy(), kt.copy(), vt.copy()
+    m.close()
+    monkeypatch.setenv("TALOS_HIP_PF_TILED", "0")
+    _step(f"{which}: {n}-token prompt, row-major weights")
+    m = talos.Model.synth(wl.spec, nthreads=16)
+    lr, ar = m.prefill(prompt, 0)
+    kr, vr = m.kv_read(n)
+    assert at == ar
+    assert np.array_equal(lt, lr) and np.array_equal(kt, kr) and np.array_equal(vt, vr)
+    ref = oracle.OracleModel(m.gguf_view(), nthreads=16)
+    for p, t in enumerate(prompt):
+        c = ref.forward(t, p)
+    kc, vc = ref.get_kv(n)
+    d = float(np.abs(lt - c).max())
+    dk = float(max(np.abs(kt - kc).max(), np.abs(vt - vc).max()))
+    print(f"  tiled == row-major bit for bit; last logits max abs {d:.3e}, K/V max abs {dk:.3e}", flush=True)
+    assert d <= 1e-3 and dk <= 1e-3 and at == oracle.argmax(c)
+    record_parity(f"{which}_tiled_weights_prefill_{n}", max(d, dk), 1e-3, path="batched_prefill")
+    ref.close()
+    m.close()
