@@ -127,7 +127,11 @@ int talos_hip_decode_greedy(talos_hip_ctx* ctx, uint32_t token, uint32_t pos, ui
  * from a device copy of `tokens` (bit-identical to a host loop of
  * talos_hip_forward_token).  Returns the last step's logits (nullable) and
  * argmax (nullable), which is the first greedy token.  pos + n must be
- * <= context_length and every token < vocab_size. */
+ * <= context_length and every token < vocab_size.  The first batched call
+ * also makes the prefill GEMMs' tiled copy of the Q4_0 / Q8_0 layer
+ * matrices (one more device copy of them, kept until a weight is uploaded
+ * or the context destroyed; none with TALOS_HIP_PF_TILED=0 in the
+ * environment when the context is created). */
 int talos_hip_prefill(talos_hip_ctx* ctx, const uint32_t* tokens, uint32_t n, uint32_t pos, float* logits,
                       uint32_t* argmax);
 
