@@ -388,8 +388,10 @@ def lc_measure(args) -> dict:
            "prefill": {"seconds": round(prefill_s, 3), "projection_flops": gemm_f, "attention_flops": attn_f,
                        "achieved_tflops": round((gemm_f + attn_f) / prefill_s / 1e12, 1),
                        "note": "projections on f16 matrix cores with x split into hi + lo halves (two "
-                               "MFMAs per product), attention on f16 matrix cores with q, K, V and the "
-                               "probabilities split (three MFMAs per product); f16 MFMA peak 2500 TFLOP/s"},
+                               "MFMAs per product), reading tile-contiguous copies of the layer matrices "
+                               "(made by the warm-up prefill), attention on f16 matrix cores with q, K, V "
+                               "and the probabilities split (three MFMAs per product); f16 MFMA peak "
+                               "2500 TFLOP/s"},
            "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(k_gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": int(sbytes),
                         "us_per_launch": round(us, 2), "pos": mid},
