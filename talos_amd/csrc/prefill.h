@@ -55,21 +55,58 @@ __global__ __launch_bounds__(256) void k_pf_embed(DevMat M, const int32_t* __res
 }
 
 // Xn_t = rmsnorm(x_t) * w (src/math/ops.rs:5-12), one row per block; with
-// X16 also in the split-f16 GEMM's interleaved halves.
+// X16 also in the split-f16 GEMM's interleaved halves.  n % 8 == 0: each
+// thread takes 8-element groups with 16-byte loads and stores, a group's 8
+// hi and 8 lo halves as two 16-byte words (the sum of squares in another
+// order than the scalar loop's, within f32 rounding of it).
 __global__ __launch_bounds__(256) void k_pf_rmsnorm(const float* __restrict__ X, const float* __restrict__ w,
                                                     float eps, uint32_t n, float* __restrict__ Xn,
                                                     uint16_t* __restrict__ X16) {
   __shared__ float red[8];
-  const float* x = X + (size_t)blockIdx.x * n;
+  const size_t ro = (size_t)blockIdx.x * n;
+  const float* x = X + ro;
+  if (n % 8 == 0) {
+    const uint32_t n8 = n / 8;
+    const f4* x4 = reinterpret_cast<const f4*>(x);
+    float ss = 0.f;
+    for (uint32_t gi = threadIdx.x; gi < n8; gi += 256) {
+      const f4 a = x4[2 * gi], b = x4[2 * gi + 1];
+      ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) + ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+    }
+    ss = block_sum(ss, red, 4);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    const f4* w4 = reinterpret_cast<const f4*>(w);
+    f4* y4 = reinterpret_cast<f4*>(Xn + ro);
+    for (uint32_t gi = threadIdx.x; gi < n8; gi += 256) {
+      const f4 a = x4[2 * gi], b = x4[2 * gi + 1], wa = w4[2 * gi], wb = w4[2 * gi + 1];
+      const float v[8] = {a.x * scale * wa.x, a.y * scale * wa.y, a.z * scale * wa.z, a.w * scale * wa.w,
+                          b.x * scale * wb.x, b.y * scale * wb.y, b.z * scale * wb.z, b.w * scale * wb.w};
+      y4[2 * gi] = f4{v[0], v[1], v[2], v[3]};
+      y4[2 * gi + 1] = f4{v[4], v[5], v[6], v[7]};
+      if (X16) {
+        uint16_t hi[8], lo[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pf16_split_bits(v[k], hi[k], lo[k]);
+        auto pack = [](const uint16_t(&h)[8]) {
+          return u4{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                    (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
+        };
+        u4* d = reinterpret_cast<u4*>(X16 + pf16_x_at(ro, 8 * gi));
+        d[0] = pack(hi);
+        d[1] = pack(lo);
+      }
+    }
+    return;
+  }
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < n; i += 256) ss += x[i] * x[i];
   ss = block_sum(ss, red, 4);
   const float scale = 1.0f / sqrtf(ss / (float)n + eps);
   for (uint32_t i = threadIdx.x; i < n; i += 256) {
     const float v = x[i] * scale * w[i];
-    Xn[(size_t)blockIdx.x * n + i] = v;
+    Xn[ro + i] = v;
     if (X16) {
-      const size_t at = pf16_x_at((size_t)blockIdx.x * n, i);
+      const size_t at = pf16_x_at(ro, i);
       pf16_split_bits(v, X16[at], X16[at + 8]);
     }
   }
