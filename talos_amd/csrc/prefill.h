@@ -688,19 +688,31 @@ __global__ __launch_bounds__(PF_NT) void k_pf_gemm16(PfGemm G) {
   }
 }
 
-// RoPE of the raw q and k rows of T tokens at positions p0 + t (any
-// head_dim, as k_rope_qkv), the K and V rows into the cache.
+// RoPE of the raw q and k rows of T tokens at positions p0 + t, the K and V
+// rows into the cache: four consecutive elements (two rotation pairs of one
+// head) per thread with 16-byte loads and stores, head_dim % 4 == 0 (the
+// batched prefill takes head_dim % 16 == 0); rope_elem's arithmetic.
 __global__ __launch_bounds__(256) void k_pf_rope_kv(const float* __restrict__ Qr, const float* __restrict__ Kr,
                                                     const float* __restrict__ Vr, float* __restrict__ Q,
                                                     float* __restrict__ kc, float* __restrict__ vc,
                                                     const float* __restrict__ rope, uint32_t p0, uint32_t n,
                                                     uint32_t n_head, uint32_t hd, uint32_t kv_dim) {
-  const uint32_t t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t t = blockIdx.y, i = (blockIdx.x * 256 + threadIdx.x) * 4;
   const int pos = (int)(p0 + t);
-  if (i < n) Q[(size_t)t * n + i] = i < n_head * hd ? rope_elem(Qr + (size_t)t * n, i, hd, pos, rope) : Qr[(size_t)t * n + i];
+  const uint32_t half = hd / 2;
+  // pairs p, p + 1 of the head (p even, so the table's 4 floats are aligned)
+  auto rot = [&](const f4 v) {
+    const uint32_t p = (i % hd) / 2;
+    const f4 cs = *reinterpret_cast<const f4*>(rope + ((size_t)pos * half + p) * 2);
+    return f4{v.x * cs.x - v.y * cs.y, v.x * cs.y + v.y * cs.x, v.z * cs.z - v.w * cs.w, v.z * cs.w + v.w * cs.z};
+  };
+  if (i < n) {
+    const f4 v = *reinterpret_cast<const f4*>(Qr + (size_t)t * n + i);
+    *reinterpret_cast<f4*>(Q + (size_t)t * n + i) = i < n_head * hd ? rot(v) : v;
+  }
   if (i < kv_dim) {
-    kc[(size_t)pos * kv_dim + i] = rope_elem(Kr + (size_t)t * kv_dim, i, hd, pos, rope);
-    vc[(size_t)pos * kv_dim + i] = Vr[(size_t)t * kv_dim + i];
+    *reinterpret_cast<f4*>(kc + (size_t)pos * kv_dim + i) = rot(*reinterpret_cast<const f4*>(Kr + (size_t)t * kv_dim + i));
+    *reinterpret_cast<f4*>(vc + (size_t)pos * kv_dim + i) = *reinterpret_cast<const f4*>(Vr + (size_t)t * kv_dim + i);
   }
 }
 

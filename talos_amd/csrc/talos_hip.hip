@@ -1349,7 +1349,7 @@ int pf_chunk(talos_hip_ctx* c, const uint32_t* tokens, uint32_t T, uint32_t p0) 
     hipLaunchKernelGGL(k_pf_rmsnorm, dim3(T), dim3(256), 0, c->stream, c->pf_x, w.an, cf.rms_eps, n, c->pf_xn,
                        c->pf_xn16);
     enq_gemm(c, {{w.q, c->pf_qr, n}, {w.k, c->pf_kr, kv}, {w.v, c->pf_vr, kv}}, xn, T, 0);
-    hipLaunchKernelGGL(k_pf_rope_kv, dim3((std::max(n, kv) + 255) / 256, T), dim3(256), 0, c->stream, c->pf_qr,
+    hipLaunchKernelGGL(k_pf_rope_kv, dim3((std::max(n, kv) / 4 + 255) / 256, T), dim3(256), 0, c->stream, c->pf_qr,
                        c->pf_kr, c->pf_vr, c->pf_q, c->kc[l], c->vc[l], c->rope, p0, n, cf.n_head, c->hd, kv);
     enq_pf_attn(c, l, T, p0);
     enq_gemm(c, {{w.o, c->pf_x, n}}, {c->pf_att, c->pf_att16}, T, 1);
